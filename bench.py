@@ -1,0 +1,332 @@
+#!/usr/bin/env python3
+"""Decode-step benchmark of the quantized Nemotron-H-8B paths on one MI355X.
+
+One step = the quantized work of one decode step of the hybrid stack at batch 64, context 16384:
+  4 attention layers:  INT4 pack of the new K and V token (2 calls) + q_len=1 decode attention
+                       over the packed cache (32 query / 8 KV heads, head_dim 128, group 32)
+  24 Mamba2 layers:    fused MX4 selective-state update (128 heads x 64 x 128, 8 groups,
+                       stochastic writeback from the counter generator)
+Every layer owns its own cache / state (about 8 GB in total), so no buffer is reused within a
+step and the 256 MB Infinity Cache cannot hold a layer's data between its uses. Inputs are
+synthetic (random packed caches with fp32 scales, N(0, 0.5) states, N(0, 1) activations) and
+resident in HBM before the timed region.
+
+Prints one JSON line: value = microseconds per step (lower is better), per-kernel HIP-event
+timings over the timed steps, the roofline of the dominant kernel, and the CPU oracle timed on a
+bounded sample of the same work on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = ("µs/decode-step & achieved HBM GB/s (frac of 8 TB/s): INT4 attn, MX8/MX4 state")
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--ctx", type=int, default=16384)
+    ap.add_argument("--group", type=int, default=32)
+    ap.add_argument("--attn-layers", type=int, default=4)
+    ap.add_argument("--mamba-layers", type=int, default=24)
+    ap.add_argument("--state-bits", type=int, default=4, choices=[4, 8])
+    ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    return ap.parse_args()
+
+
+class Events:
+    """Pairs of timing events recorded on the current stream around each kernel call."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs: dict[str, list] = {}
+
+    def around(self, name, fn):
+        t = self.torch
+        a = t.cuda.Event(enable_timing=True)
+        b = t.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        self.pairs.setdefault(name, []).append((a, b))
+
+    def mean_us(self, name):
+        pairs = self.pairs.get(name, [])
+        if not pairs:
+            return None
+        return 1000.0 * sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
+
+
+def build_workload(torch, args, dev):
+    from layer_quant_amd import _abi
+    from oracle.int4_kv import algorithmic_bytes, pack_algorithmic_bytes
+    from oracle.mx_state import update_algorithmic_bytes
+
+    B, S, g = args.batch, args.ctx, args.group
+    hq, hkv, d = 32, 8, 128
+    nh, p_, n, ng = 128, 64, 128, 8
+    gen = torch.Generator(device=dev).manual_seed(0)
+    attn = []
+    for _ in range(args.attn_layers):
+        layer = dict(
+            k_packed=torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev,
+                                   generator=gen),
+            v_packed=torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev,
+                                   generator=gen),
+            k_scale=torch.rand(B, hkv, S, d // g, device=dev, generator=gen) * 0.5 + 0.01,
+            v_scale=torch.rand(B, hkv, S, d // g, device=dev, generator=gen) * 0.5 + 0.01,
+            q=torch.randn(B, hq, 1, d, device=dev, generator=gen).to(torch.bfloat16),
+            k_new=torch.randn(B, hkv, 1, d, device=dev, generator=gen).to(torch.bfloat16),
+            v_new=torch.randn(B, hkv, 1, d, device=dev, generator=gen).to(torch.bfloat16),
+            out=torch.empty(B, hq, d, device=dev, dtype=torch.bfloat16),
+            pos=torch.full((1,), S - 1, dtype=torch.long, device=dev),
+        )
+        attn.append(layer)
+    mamba = []
+    for _ in range(args.mamba_layers):
+        h0 = torch.randn(B, nh, p_, n, device=dev, generator=gen) * 0.5
+        st = (torch.empty(B, nh, p_, n, dtype=torch.int8, device=dev),
+              torch.empty(B, nh, p_, n // 16, dtype=torch.uint8, device=dev),
+              torch.empty(B, nh, p_, n // 2, dtype=torch.uint8, device=dev))
+        _abi.mx_encode(h0, *st, args.state_bits, _abi.ROUND_NEAREST_EVEN)
+        del h0
+        layer = dict(
+            st=st,
+            x=torch.randn(B, nh, p_, device=dev, generator=gen).to(torch.bfloat16),
+            dt=torch.randn(B, nh, device=dev, generator=gen).to(torch.bfloat16)[:, :, None]
+            .expand(B, nh, p_),
+            A=(-torch.exp(torch.rand(nh, device=dev, generator=gen) * 2))[:, None, None]
+            .expand(nh, p_, n),
+            B=torch.randn(B, ng, n, device=dev, generator=gen).to(torch.bfloat16),
+            C=torch.randn(B, ng, n, device=dev, generator=gen).to(torch.bfloat16),
+            D=torch.randn(nh, device=dev, generator=gen)[:, None].expand(nh, p_),
+            dt_bias=(torch.randn(nh, device=dev, generator=gen) * 0.1)[:, None].expand(nh, p_),
+            out=torch.empty(B, nh, p_, device=dev, dtype=torch.bfloat16),
+            step=0,
+        )
+        mamba.append(layer)
+    torch.cuda.synchronize()
+    sizes = dict(
+        attention=algorithmic_bytes(B, hq, hkv, d, S, g),
+        pack=pack_algorithmic_bytes(B, hkv, 1, d, g),
+        mx_update=update_algorithmic_bytes(B, nh, p_, n, ng),
+    )
+    return attn, mamba, sizes
+
+
+def run_step(torch, args, attn, mamba, ev=None):
+    from layer_quant_amd import _abi
+
+    B, S, g = args.batch, args.ctx, args.group
+    total_state = B * 128 * 64 * 128
+
+    def call(name, fn):
+        if ev is None:
+            fn()
+        else:
+            ev.around(name, fn)
+
+    for L in attn:
+        call("pack", lambda: _abi.int4_pack_kv(L["k_new"], L["k_packed"], L["k_scale"], L["pos"], g))
+        call("pack", lambda: _abi.int4_pack_kv(L["v_new"], L["v_packed"], L["v_scale"], L["pos"], g))
+        call("attention", lambda: _abi.int4_decode_attention(
+            L["q"], L["k_packed"], L["v_packed"], L["k_scale"], L["v_scale"], None, L["out"], S,
+            4, g))
+    for M in mamba:
+        off = M["step"] * total_state
+        call("mx_update", lambda: _abi.mx_state_update(
+            *M["st"], M["x"], M["dt"], M["dt_bias"], M["A"], M["B"], M["C"], M["D"], None,
+            M["out"], args.state_bits, True, _abi.ROUND_SR_COUNTER, seed=1234, rng_offset=off))
+        M["step"] += 1
+
+
+def cpu_baseline(args):
+    """The CPU oracle (torch fp32/fp64 restatement of the reference formulas) on a bounded
+    sample of the same step, on this host's cores, scaled linearly to the full step."""
+    import numpy as np
+    import torch
+
+    from oracle import int4_kv as oik
+    from oracle import mx_state as omx
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    gen = torch.Generator().manual_seed(0)
+    hq, hkv, d, g = 32, 8, 128, args.group
+    s_sample = min(args.ctx, 4096)
+    cache = oik.allocate_cache(1, hkv, s_sample, d, g)
+    kv = torch.randn(1, hkv, s_sample, d, generator=gen).to(torch.bfloat16)
+    oik.pack_kv_into_cache(cache, kv, kv, torch.arange(s_sample), g)
+    q = torch.randn(1, hq, 1, d, generator=gen).to(torch.bfloat16)
+    new = torch.randn(1, hkv, 1, d, generator=gen).to(torch.bfloat16)
+
+    def attn_once():
+        oik.pack_into(cache["k_packed"], cache["k_scale"], new, torch.tensor([s_sample - 1]), g)
+        oik.pack_into(cache["v_packed"], cache["v_scale"], new, torch.tensor([s_sample - 1]), g)
+        oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
+                             cache["v_scale"], s_sample, 4, g)
+
+    b_sample = 2
+    shape = (b_sample, 128, 64, 128)
+    qs, es, ms_ = omx.mx_encode((torch.randn(shape, generator=gen) * 0.5).numpy(), args.state_bits)
+    x = torch.randn(b_sample, 128, 64, generator=gen).to(torch.bfloat16)
+    dt = torch.randn(b_sample, 128, 64, generator=gen).to(torch.bfloat16)
+    A = -torch.rand(128, generator=gen)[:, None, None].expand(128, 64, 128)
+    Bm = torch.randn(b_sample, 8, 128, generator=gen).to(torch.bfloat16)
+    D = torch.randn(128, generator=gen)[:, None].expand(128, 64)
+
+    def mx_once():
+        omx.mx_update(qs, es, ms_, x, dt, A, Bm, Bm, D=D, dt_bias=D * 0.1, dt_softplus=True,
+                      format_bits=args.state_bits, round_mode=omx.ROUND_SR_COUNTER, seed=1234)
+
+    def timed(fn, reps):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    t_attn = timed(attn_once, 3)
+    t_mx = timed(mx_once, 3)
+    scale_attn = args.batch * (args.ctx / s_sample)
+    scale_mx = args.batch / b_sample
+    step_s = args.attn_layers * t_attn * scale_attn + args.mamba_layers * t_mx * scale_mx
+    return {
+        "value": round(step_s * 1e6, 1),
+        "unit": "us/step",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"oracle (torch/numpy CPU) on 1 attention layer at batch 1, ctx {s_sample} "
+                   f"(pack K,V + attend) and 1 MX{args.state_bits} update at batch {b_sample}, "
+                   f"median of 3, scaled linearly to {args.attn_layers} layers x batch "
+                   f"{args.batch} x ctx {args.ctx} and {args.mamba_layers} layers x batch "
+                   f"{args.batch}; attention {t_attn * 1e3:.1f} ms, update {t_mx * 1e3:.1f} ms"),
+    }
+
+
+def load_traffic(kernel: str, workload: str):
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        data = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = data.get(kernel, {})
+    if entry.get("workload") != workload:
+        return None
+    return entry.get("bytes_per_launch")
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the path has no multi-GPU component in this build)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    log(f"building workload: batch {args.batch}, ctx {args.ctx}, {args.attn_layers} attention "
+        f"+ {args.mamba_layers} MX{args.state_bits} layers")
+    attn, mamba, sizes = build_workload(torch, args, dev)
+    log("warmup")
+    for _ in range(args.warmup):
+        run_step(torch, args, attn, mamba)
+    torch.cuda.synchronize()
+
+    # timed region 1: whole steps, no per-kernel events
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run_step(torch, args, attn, mamba)
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+    log(f"step: {step_s * 1e6:.1f} us")
+
+    # timed region 2: the same steps with HIP events around every kernel call
+    ev = Events(torch)
+    for _ in range(args.steps):
+        run_step(torch, args, attn, mamba, ev)
+    torch.cuda.synchronize()
+    kernels = {}
+    for name, nbytes in sizes.items():
+        us = ev.mean_us(name)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        kernels[name] = {"us": round(us, 2), "algorithmic_bytes": nbytes,
+                         "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+                         "calls_per_step": {"attention": args.attn_layers,
+                                            "pack": 2 * args.attn_layers,
+                                            "mx_update": args.mamba_layers}[name]}
+        log(f"{name}: {us:.1f} us/call, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%})")
+    dominant = max(kernels, key=lambda k: kernels[k]["us"] * kernels[k]["calls_per_step"])
+    dk = kernels[dominant]
+    workload = f"b{args.batch}_ctx{args.ctx}_g{args.group}_mx{args.state_bits}"
+    roofline = {
+        "kernel": {"attention": "lq_int4_decode_attention (attn_fast_kernel + attn_merge_kernel)",
+                   "mx_update": f"lq_mx_state_update (mx_update_kernel MX{args.state_bits})",
+                   "pack": "lq_int4_pack_kv"}[dominant],
+        "bound": "hbm",
+        "achieved": dk["GB_s"],
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": dk["frac_of_peak"],
+        "traffic": load_traffic(dominant, workload),
+    }
+    cpu = None
+    if args.cpu_baseline == "on":
+        log("cpu baseline")
+        cpu = cpu_baseline(args)
+    line = {
+        "metric": METRIC,
+        "value": round(step_s * 1e6, 1),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"Nemotron-H-8B decode step, quantized paths only: {args.attn_layers} "
+                         f"INT4-KV attention layers (32q/8kv heads, head_dim 128, group "
+                         f"{args.group}, ctx {args.ctx}) with their K/V packs + "
+                         f"{args.mamba_layers} MX{args.state_bits} Mamba2 state updates "
+                         "(128 heads x 64 x 128, 8 groups, stochastic writeback)"),
+            "batch": args.batch,
+            "ctx": args.ctx,
+            "group_size": args.group,
+            "state_format": f"mx{args.state_bits}",
+        },
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,163 @@
+/*
+ * layer_quant.h -- C ABI of the MI355X (gfx950) decode-path kernels.
+ *
+ * One shared library (liblayer_quant.so) exports the entry points below. They replace the
+ * Triton kernel launches of the reference's two quantized decode paths:
+ *
+ *   hybrid_quant/int4_8b_attention.py     INT4 KV cache: per-token pack + q_len=1 decode attention
+ *   hybrid_quant/mamba_state_8b_kernel.py Mamba2 selective-state update over an MX8/MX4 state
+ *
+ * Conventions
+ *   - The caller owns every buffer. The library never allocates device memory; scratch space
+ *     (split-K partials) comes from a caller workspace sized by a query function.
+ *   - Every launch is asynchronous on the caller's HIP stream, passed as `void* stream`
+ *     (a hipStream_t; NULL is the legacy default stream). No entry point synchronizes.
+ *   - Tensors are described by lq_tensor: a device pointer, a dtype code, a rank (1..4), a shape
+ *     and strides counted in ELEMENTS (not bytes). Strides may be 0 (broadcast views).
+ *   - Return value: 0 on success, a negative LQ_ERR_* code on failure. lq_last_error() returns a
+ *     thread-local message describing the last failure on the calling thread. Argument
+ *     validation happens before any HIP call, so invalid arguments never touch the device.
+ */
+#ifndef LAYER_QUANT_H_
+#define LAYER_QUANT_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LQ_ABI_VERSION 1
+
+/* dtype codes for lq_tensor.dtype */
+enum {
+  LQ_U8 = 0,
+  LQ_I8 = 1,
+  LQ_F16 = 2,
+  LQ_BF16 = 3,
+  LQ_F32 = 4,
+  LQ_I32 = 5,
+  LQ_I64 = 6
+};
+
+/* error codes */
+enum {
+  LQ_OK = 0,
+  LQ_ERR_INVALID_ARG = -1,
+  LQ_ERR_UNSUPPORTED = -2,
+  LQ_ERR_WORKSPACE = -3,
+  LQ_ERR_HIP = -4
+};
+
+/* rounding modes of the MX encoders */
+enum {
+  LQ_ROUND_NEAREST_EVEN = 0, /* torch.round of clamp(|v|/scale, 0, M): the initial encode       */
+  LQ_ROUND_HALF_UP = 1,      /* floor(min(|v|/scale, M) + 0.5): the deterministic writeback     */
+  LQ_ROUND_SR_UNIFORM = 2,   /* floor(q) + (u < q - floor(q)), u from a caller fp32 tensor       */
+  LQ_ROUND_SR_COUNTER = 3    /* same comparison, u from the library's counter-based generator    */
+};
+
+typedef struct lq_tensor {
+  void* data;
+  int32_t dtype;
+  int32_t ndim;
+  int64_t shape[4];
+  int64_t stride[4];
+} lq_tensor;
+
+/* ABI version (LQ_ABI_VERSION) of the loaded library. */
+int lq_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* lq_last_error(void);
+
+/*
+ * INT4 pack of new K or V tokens into the packed cache.
+ * Replaces the launch of _pack_int4_kv_kernel (reference hybrid_quant/int4_8b_attention.py:32-111,
+ * launched twice by _pack_kv_into_cache at :477-514).
+ *   x         [B, Hkv, q_len, D]  f32/f16/bf16, any strides
+ *   packed    [B, Hkv, cap, D/2]  u8   (byte p holds d=2p in the low nibble, d=2p+1 in the high)
+ *   scale     [B, Hkv, cap, D/g]  f32
+ *   positions [q_len]             i64  cache row written for each new token
+ * Per group of g values: scale = max(absmax/7, 1e-8); q = clamp(rint(x/scale), -8, 7).
+ * Rows outside [0, cap) are skipped (the caller grows the cache first).
+ */
+int lq_int4_pack_kv(const lq_tensor* x, const lq_tensor* packed, const lq_tensor* scale,
+                    const lq_tensor* positions, int group_size, void* stream);
+
+/*
+ * Workspace bytes that lq_int4_decode_attention needs for this shape (0 if none).
+ * No counterpart in the reference (its decode kernel has no split-K); it sizes the split-K
+ * partials of the kernel below.
+ */
+size_t lq_int4_decode_attention_workspace(int64_t batch, int64_t n_q_heads, int64_t n_kv_heads,
+                                          int64_t head_dim, int64_t seq_len, int group_size);
+
+/*
+ * q_len = 1 GQA attention over the packed INT4 cache.
+ * Replaces the launch of _int4_decode_attention_kernel (reference
+ * hybrid_quant/int4_8b_attention.py:254-402, launched by _decode_attention at :518-566).
+ *   q         [B, Hq, 1, D] or [B, Hq, D]   f32/f16/bf16
+ *   k_packed, v_packed [B, Hkv, cap, D/2] u8;  k_scale, v_scale [B, Hkv, cap, D/g] f32
+ *   mask      NULL or [B, 1, 1, Lm] f32 additive bias (only batch and key strides are used;
+ *             keys at or beyond Lm get -inf, as in the reference)
+ *   out       [B, Hq, D]   f32/f16/bf16
+ * Keys [0, seq_len) are attended; q head h reads KV head h / num_key_value_groups.
+ * Scores use exp2 with scale log2(e)/sqrt(D); softmax and accumulation are fp32.
+ */
+int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
+                             const lq_tensor* v_packed, const lq_tensor* k_scale,
+                             const lq_tensor* v_scale, const lq_tensor* mask, const lq_tensor* out,
+                             int64_t seq_len, int num_key_value_groups, int group_size,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * MX block encode of a float state [B, H, P, N] (N % 16 == 0) into the reference's MX layout:
+ *   q_state [B,H,P,N] i8 (one byte per mantissa, also for MX4), shared_exp [B,H,P,N/16] u8
+ *   (biased, 127 = 2^0), micro_exp [B,H,P,N/2] u8 (0/1 per pair).
+ * format_bits 8 -> mantissa max 63, 4 -> 7. With LQ_ROUND_NEAREST_EVEN this replaces
+ * _quantize_initial_state_mx (reference hybrid_quant/mamba_state_8b_kernel.py:547-572); the
+ * other modes run the writeback encoder of :168-222 / :494-544 on a given state.
+ *   uniform    [B,H,P,N] f32, required for LQ_ROUND_SR_UNIFORM, else NULL
+ *   seed, rng_offset: counter of LQ_ROUND_SR_COUNTER (element (b,h,p,n) draws counter
+ *   rng_offset + ((b*H + h)*P + p)*N + n)
+ */
+int lq_mx_encode(const lq_tensor* state, const lq_tensor* q_state, const lq_tensor* shared_exp,
+                 const lq_tensor* micro_exp, int format_bits, int round_mode,
+                 const lq_tensor* uniform, uint64_t seed, uint64_t rng_offset, void* stream);
+
+/*
+ * Dequantize an MX state: out[b,h,p,n] = q * 2^(shared_exp - 127 + micro_exp) (f32/bf16 out).
+ * No kernel of its own in the reference (its update kernels decode inline at
+ * hybrid_quant/mamba_state_8b_kernel.py:132 and :322); used to read a state back.
+ */
+int lq_mx_decode(const lq_tensor* q_state, const lq_tensor* shared_exp,
+                 const lq_tensor* micro_exp, const lq_tensor* out, void* stream);
+
+/*
+ * Fused Mamba2 selective-state update over an MX8/MX4 state, in place:
+ *   h  = q * 2^(e - 127 + micro)
+ *   dt = dt (+ dt_bias); dt = softplus(dt) if dt_softplus (x <= 20 ? log(1+e^x) : x)
+ *   h' = h * exp(A * dt) + (B * dt) * x;   y = sum_n h' * C (+ x * D) (* z)
+ *   re-encode h' (format_bits 8 or 4) with round_mode, write y to out.
+ * Replaces _state_update_requant_mx8_row_kernel (reference
+ * hybrid_quant/mamba_state_8b_kernel.py:33-222) for MX8 and the pair
+ * _state_update_mx8_kernel + _requantize_mx4_kernel (:225-443, :494-544) for MX4, as dispatched
+ * by mx_state_selective_update (:601-721). One pass: no fp32 temporary state.
+ *   x [B,H,P]; dt [B,H,P]; dt_bias NULL or [H,P]; A [H,P,N] f32; B, C [B,G,N] with H % G == 0;
+ *   D NULL or [H,P]; z NULL or [B,H,P]; out [B,H,P]. Any strides (0 allowed) on these.
+ *   q_state/shared_exp/micro_exp: innermost dimension contiguous.
+ */
+int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* shared_exp,
+                       const lq_tensor* micro_exp, const lq_tensor* x, const lq_tensor* dt,
+                       const lq_tensor* dt_bias, const lq_tensor* A, const lq_tensor* B,
+                       const lq_tensor* C, const lq_tensor* D, const lq_tensor* z,
+                       const lq_tensor* out, int format_bits, int dt_softplus, int round_mode,
+                       const lq_tensor* uniform, uint64_t seed, uint64_t rng_offset, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LAYER_QUANT_H_ */

@@ -1,0 +1,336 @@
+// q_len = 1 GQA decode attention over the packed INT4 KV cache.
+//
+// Replaces _int4_decode_attention_kernel (reference hybrid_quant/int4_8b_attention.py:254-402).
+// Two kernels share one split-K plan and one merge:
+//   * attn_fast_kernel (int4_attention_mfma.hip): head_dim 128, group 32/64/128, all query heads
+//     of a KV head in one MFMA tile; every KV byte is read once per (batch, KV head).
+//   * attn_generic_kernel (here): any even group dividing any head_dim <= 512, one wave per
+//     (batch, query head, split), fp32 VALU throughout.
+// Scores follow the reference: s_n = (q . k_n) * log2(e)/sqrt(D) (+ mask_n), exp2-domain online
+// softmax; keys at or beyond the mask length get -inf. Splits write (m, l, acc[D]) partials into
+// the caller's workspace and attn_merge_kernel combines them; a single split writes out directly.
+#include <math.h>
+
+#include "int4_attention.h"
+
+namespace lq {
+
+constexpr int GEN_MAX_D = 512;
+
+__global__ __launch_bounds__(64) void attn_generic_kernel(AttnParams p) {
+  __shared__ float q_s[GEN_MAX_D];
+  __shared__ float p_s[64];
+  const int lane = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int split = blockIdx.y;
+  const int b = bh / p.Hq;
+  const int qh = bh - b * p.Hq;
+  const int kvh = qh / p.nrep;
+  const int64_t t0 = (int64_t)split * p.chunk;
+  const int64_t t1 = min(p.S, t0 + p.chunk);
+  const int D = p.D;
+  const int g = p.g;
+
+  for (int d = lane; d < D; d += 64) {
+    q_s[d] = load_float(p.q.data, p.q.dtype, b * p.q.s[0] + qh * p.q.s[1] + d * p.q.s[2]);
+  }
+  __syncthreads();
+
+  const uint8_t* kbase = p.kp + b * p.kps[0] + kvh * p.kps[1];
+  const uint8_t* vbase = p.vp + b * p.vps[0] + kvh * p.vps[1];
+  const float* ksbase = p.ks + b * p.kss[0] + kvh * p.kss[1];
+  const float* vsbase = p.vs + b * p.vss[0] + kvh * p.vss[1];
+  const int groups = D / g;
+
+  float m = -INFINITY;
+  float l = 0.0f;
+  float acc[GEN_MAX_D / 64];
+#pragma unroll
+  for (int i = 0; i < GEN_MAX_D / 64; ++i) acc[i] = 0.0f;
+
+  for (int64_t start = t0; start < t1; start += 64) {
+    const int64_t n = start + lane;
+    float s = -INFINITY;
+    if (n < t1) {
+      const uint8_t* kr = kbase + n * p.kps[2];
+      const float* ksr = ksbase + n * p.kss[2];
+      float tot = 0.0f;
+      for (int gi = 0; gi < groups; ++gi) {
+        float part = 0.0f;
+        for (int d = gi * g; d < (gi + 1) * g; d += 2) {
+          const int byte = kr[(d >> 1) * p.kps[3]];
+          int lo = byte & 15;
+          int hi = (byte >> 4) & 15;
+          lo = lo >= 8 ? lo - 16 : lo;
+          hi = hi >= 8 ? hi - 16 : hi;
+          part += q_s[d] * (float)lo + q_s[d + 1] * (float)hi;
+        }
+        tot += part * ksr[gi * p.kss[3]];
+      }
+      s = tot * p.scale_sm;
+      if (p.mask != nullptr) {
+        s += (n < p.mask_len) ? p.mask[b * p.mask_sb + n * p.mask_sk] : -INFINITY;
+      }
+    }
+    const float mt = group_max<64>(s);
+    const float m_new = fmaxf(m, mt);
+    const float alpha = (m_new == -INFINITY) ? 1.0f : exp2f(m - m_new);
+    const float pn = (s == -INFINITY) ? 0.0f : exp2f(s - m_new);
+    l = l * alpha + group_sum<64>(pn);
+    p_s[lane] = pn;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < GEN_MAX_D / 64; ++i) acc[i] *= alpha;
+    const int cnt = (int)min((int64_t)64, t1 - start);
+    for (int j = 0; j < cnt; ++j) {
+      const float pj = p_s[j];
+      const uint8_t* vr = vbase + (start + j) * p.vps[2];
+      const float* vsr = vsbase + (start + j) * p.vss[2];
+#pragma unroll
+      for (int i = 0; i < GEN_MAX_D / 64; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) {
+          const int byte = vr[(d >> 1) * p.vps[3]];
+          int nib = (d & 1) ? ((byte >> 4) & 15) : (byte & 15);
+          nib = nib >= 8 ? nib - 16 : nib;
+          acc[i] += pj * ((float)nib * vsr[(d / g) * p.vss[3]]);
+        }
+      }
+    }
+    __syncthreads();
+    m = m_new;
+  }
+
+  if (p.nsplit == 1) {
+#pragma unroll
+    for (int i = 0; i < GEN_MAX_D / 64; ++i) {
+      const int d = lane + 64 * i;
+      if (d < D) store_float(p.out.data, p.out.dtype, b * p.out.s[0] + qh * p.out.s[1] + d * p.out.s[2], acc[i] / l);
+    }
+  } else {
+    const int64_t slot = (int64_t)bh * p.nsplit + split;
+    if (lane == 0) {
+      p.ws_m[slot] = m;
+      p.ws_l[slot] = l;
+    }
+#pragma unroll
+    for (int i = 0; i < GEN_MAX_D / 64; ++i) {
+      const int d = lane + 64 * i;
+      if (d < D) p.ws_acc[slot * D + d] = acc[i];
+    }
+  }
+}
+
+// Combines the split partials of one (batch, query head): M = max m_s, w_s = 2^(m_s - M),
+// out = sum w_s acc_s / sum w_s l_s. A split with m_s = -inf (all keys masked) has weight 0.
+__global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams p) {
+  const int lane = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int b = bh / p.Hq;
+  const int qh = bh - b * p.Hq;
+  const int64_t base = (int64_t)bh * p.nsplit;
+  float M = -INFINITY;
+  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, p.ws_m[base + s]);
+  float L = 0.0f;
+  float acc[GEN_MAX_D / 64];
+#pragma unroll
+  for (int i = 0; i < GEN_MAX_D / 64; ++i) acc[i] = 0.0f;
+  for (int s = 0; s < p.nsplit; ++s) {
+    const float ms = p.ws_m[base + s];
+    const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
+    L += w * p.ws_l[base + s];
+    const float* a = p.ws_acc + (base + s) * p.D;
+#pragma unroll
+    for (int i = 0; i < GEN_MAX_D / 64; ++i) {
+      const int d = lane + 64 * i;
+      if (d < p.D) acc[i] += w * a[d];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < GEN_MAX_D / 64; ++i) {
+    const int d = lane + 64 * i;
+    if (d < p.D) {
+      store_float(p.out.data, p.out.dtype, b * p.out.s[0] + qh * p.out.s[1] + d * p.out.s[2],
+                  acc[i] / L);
+    }
+  }
+}
+
+// Split plan of the generic kernel: about 2048 waves in flight, at least 64 keys per split.
+static SplitPlan plan_generic(int64_t B, int64_t Hq, int64_t S) {
+  SplitPlan sp{};
+  const int64_t rows = std::max<int64_t>(1, B * Hq);
+  int64_t want = (2048 + rows - 1) / rows;
+  const int64_t max_split = std::max<int64_t>(1, (S + 63) / 64);
+  want = std::min(std::max<int64_t>(want, 1), max_split);
+  int64_t chunk = (S + want - 1) / want;
+  chunk = ((chunk + 63) / 64) * 64;
+  sp.chunk = std::max<int64_t>(chunk, 64);
+  sp.nsplit = (int)std::max<int64_t>(1, (S + sp.chunk - 1) / sp.chunk);
+  return sp;
+}
+
+static size_t partial_bytes(int64_t B, int64_t Hq, int64_t D, int nsplit) {
+  if (nsplit <= 1) return 0;
+  const size_t slots = (size_t)(B * Hq) * (size_t)nsplit;
+  // m and l arrays, then acc; each array rounded up to 256 bytes
+  const size_t ml = ((slots * 4 + 255) / 256) * 256;
+  return 2 * ml + slots * (size_t)D * 4;
+}
+
+static void carve_workspace(AttnParams& p, void* ws) {
+  const size_t slots = (size_t)(p.B * p.Hq) * (size_t)p.nsplit;
+  const size_t ml = ((slots * 4 + 255) / 256) * 256;
+  char* base = (char*)ws;
+  p.ws_m = (float*)base;
+  p.ws_l = (float*)(base + ml);
+  p.ws_acc = (float*)(base + 2 * ml);
+}
+
+}  // namespace lq
+
+using namespace lq;
+
+extern "C" size_t lq_int4_decode_attention_workspace(int64_t batch, int64_t n_q_heads,
+                                                     int64_t n_kv_heads, int64_t head_dim,
+                                                     int64_t seq_len, int group_size) {
+  if (batch <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || seq_len <= 0) return 0;
+  const SplitPlan g = plan_generic(batch, n_q_heads, seq_len);
+  size_t need = partial_bytes(batch, n_q_heads, head_dim, g.nsplit);
+  if (fast_path_shape_ok(head_dim, group_size, n_q_heads, n_kv_heads)) {
+    const SplitPlan f = plan_fast(batch, n_kv_heads, seq_len);
+    need = std::max(need, partial_bytes(batch, n_q_heads, head_dim, f.nsplit));
+  }
+  return need;
+}
+
+extern "C" int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
+                                        const lq_tensor* v_packed, const lq_tensor* k_scale,
+                                        const lq_tensor* v_scale, const lq_tensor* mask,
+                                        const lq_tensor* out, int64_t seq_len,
+                                        int num_key_value_groups, int group_size,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if (q == nullptr) return fail(LQ_ERR_INVALID_ARG, "q: descriptor is NULL");
+  const int qdim = q->ndim;
+  if (qdim != 3 && qdim != 4) {
+    return fail(LQ_ERR_INVALID_ARG, "q: expected [B, Hq, 1, D] or [B, Hq, D], got %d dims", qdim);
+  }
+  if ((rc = check_tensor(q, "q", qdim, true)) != LQ_OK) return rc;
+  if (qdim == 4 && q->shape[2] != 1) {
+    return fail(LQ_ERR_INVALID_ARG, "Fused INT4 decode attention expects q_len=1, got %lld",
+                (long long)q->shape[2]);
+  }
+  if ((rc = check_tensor(k_packed, "k_packed", 4, false, LQ_U8)) != LQ_OK) return rc;
+  if ((rc = check_tensor(v_packed, "v_packed", 4, false, LQ_U8)) != LQ_OK) return rc;
+  if ((rc = check_tensor(k_scale, "k_scale", 4, false, LQ_F32)) != LQ_OK) return rc;
+  if ((rc = check_tensor(v_scale, "v_scale", 4, false, LQ_F32)) != LQ_OK) return rc;
+  if ((rc = check_tensor(out, "out", 3, true)) != LQ_OK) return rc;
+  const int64_t B = q->shape[0], Hq = q->shape[1], D = q->shape[qdim - 1];
+  const int64_t Hkv = k_packed->shape[1], cap = k_packed->shape[2];
+  if (group_size <= 0 || group_size % 2 != 0 || D % group_size != 0) {
+    return fail(LQ_ERR_INVALID_ARG, "head_dim=%lld must be divisible by an even group_size=%d",
+                (long long)D, group_size);
+  }
+  if (D > GEN_MAX_D || D % 2 != 0) {
+    return fail(LQ_ERR_UNSUPPORTED, "head_dim=%lld unsupported (even, <= %d)", (long long)D,
+                GEN_MAX_D);
+  }
+  if (num_key_value_groups <= 0 || Hkv * num_key_value_groups != Hq) {
+    return fail(LQ_ERR_INVALID_ARG, "n_q_heads=%lld != n_kv_heads=%lld * groups=%d",
+                (long long)Hq, (long long)Hkv, num_key_value_groups);
+  }
+  const lq_tensor* caches[2] = {k_packed, v_packed};
+  for (const lq_tensor* c : caches) {
+    if (c->shape[0] != B || c->shape[1] != Hkv || c->shape[2] != cap || c->shape[3] != D / 2) {
+      return fail(LQ_ERR_INVALID_ARG, "packed caches must be [%lld, %lld, %lld, %lld]",
+                  (long long)B, (long long)Hkv, (long long)cap, (long long)(D / 2));
+    }
+  }
+  const lq_tensor* scales[2] = {k_scale, v_scale};
+  for (const lq_tensor* s : scales) {
+    if (s->shape[0] != B || s->shape[1] != Hkv || s->shape[2] != cap ||
+        s->shape[3] != D / group_size) {
+      return fail(LQ_ERR_INVALID_ARG, "scale caches must be [%lld, %lld, %lld, %lld]",
+                  (long long)B, (long long)Hkv, (long long)cap, (long long)(D / group_size));
+    }
+  }
+  if (out->shape[0] != B || out->shape[1] != Hq || out->shape[2] != D) {
+    return fail(LQ_ERR_INVALID_ARG, "out must be [%lld, %lld, %lld]", (long long)B, (long long)Hq,
+                (long long)D);
+  }
+  if (seq_len < 1 || seq_len > cap) {
+    return fail(LQ_ERR_INVALID_ARG, "seq_len=%lld outside [1, capacity=%lld]",
+                (long long)seq_len, (long long)cap);
+  }
+  if (mask != nullptr) {
+    if ((rc = check_tensor(mask, "mask", 4, false, LQ_F32)) != LQ_OK) return rc;
+    if (mask->shape[0] != B) {
+      return fail(LQ_ERR_INVALID_ARG, "mask batch %lld != %lld", (long long)mask->shape[0],
+                  (long long)B);
+    }
+  }
+  if (B == 0 || Hq == 0) return LQ_OK;
+
+  AttnParams p{};
+  p.q.data = q->data;
+  p.q.dtype = q->dtype;
+  p.q.s[0] = q->stride[0];
+  p.q.s[1] = q->stride[1];
+  p.q.s[2] = q->stride[qdim - 1];
+  p.kp = (const uint8_t*)k_packed->data;
+  p.vp = (const uint8_t*)v_packed->data;
+  p.ks = (const float*)k_scale->data;
+  p.vs = (const float*)v_scale->data;
+  for (int i = 0; i < 4; ++i) {
+    p.kps[i] = k_packed->stride[i];
+    p.vps[i] = v_packed->stride[i];
+    p.kss[i] = k_scale->stride[i];
+    p.vss[i] = v_scale->stride[i];
+  }
+  if (mask != nullptr) {
+    p.mask = (const float*)mask->data;
+    p.mask_sb = mask->stride[0];
+    p.mask_sk = mask->stride[3];
+    p.mask_len = mask->shape[3];
+  }
+  p.out = make_view(out);
+  p.B = (int)B;
+  p.Hq = (int)Hq;
+  p.Hkv = (int)Hkv;
+  p.D = (int)D;
+  p.g = group_size;
+  p.nrep = num_key_value_groups;
+  p.S = seq_len;
+  p.scale_sm = (float)(1.4426950408889634 / sqrt((double)D));
+
+  const bool fast = fast_path_ok(p);
+  const SplitPlan sp = fast ? plan_fast(B, Hkv, seq_len) : plan_generic(B, Hq, seq_len);
+  p.nsplit = sp.nsplit;
+  p.chunk = sp.chunk;
+  const size_t need = partial_bytes(B, Hq, D, p.nsplit);
+  if (need > 0) {
+    if (workspace == nullptr || workspace_bytes < need) {
+      return fail(LQ_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
+                  workspace == nullptr ? (size_t)0 : workspace_bytes);
+    }
+    if (((uintptr_t)workspace & 255) != 0) {
+      return fail(LQ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+    }
+    carve_workspace(p, workspace);
+  }
+
+  hipStream_t st = (hipStream_t)stream;
+  if (fast) {
+    if ((rc = launch_fast(p, st)) != LQ_OK) return rc;
+  } else {
+    hipLaunchKernelGGL(attn_generic_kernel, dim3((unsigned)(B * Hq), (unsigned)p.nsplit),
+                       dim3(64), 0, st, p);
+    if ((rc = check_launch("lq_int4_decode_attention")) != LQ_OK) return rc;
+  }
+  if (p.nsplit > 1) {
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * Hq)), dim3(64), 0, st, p);
+    if ((rc = check_launch("lq_int4_decode_attention merge")) != LQ_OK) return rc;
+  }
+  return LQ_OK;
+}

@@ -1,0 +1,117 @@
+// INT4 KV pack: quantize new K or V tokens per group and write them into the packed cache.
+//
+// Replaces _pack_int4_kv_kernel (reference hybrid_quant/int4_8b_attention.py:32-111). Per group
+// of g values along head_dim: absmax -> scale = max(absmax / 7, 1e-8) -> q = rint(x / scale)
+// (IEEE division, round half to even) -> clamp [-8, 7] -> two's-complement nibbles, even d in the
+// low nibble. One thread owns one (batch, kv-head, token, group); decode writes one token per
+// call, so the kernel is launch-bound and kept simple.
+#include "lq_common.h"
+
+namespace lq {
+
+struct PackParams {
+  View x;  // [B, Hkv, T, D]
+  uint8_t* packed;
+  int64_t ps[4];  // [B, Hkv, cap, D/2]
+  float* scale;
+  int64_t ss[4];  // [B, Hkv, cap, D/g]
+  const int64_t* positions;
+  int64_t pos_stride;
+  int B, H, T, D, g;
+  int64_t cap;
+};
+
+__global__ __launch_bounds__(256) void int4_pack_kernel(PackParams p) {
+  const int groups = p.D / p.g;
+  const int64_t total = (int64_t)p.B * p.H * p.T * groups;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= total) return;
+  const int grp = (int)(gid % groups);
+  int64_t r = gid / groups;
+  const int t = (int)(r % p.T);
+  r /= p.T;
+  const int h = (int)(r % p.H);
+  const int b = (int)(r / p.H);
+  const int64_t pos = p.positions[t * p.pos_stride];
+  if (pos < 0 || pos >= p.cap) return;
+
+  const int64_t xrow = b * p.x.s[0] + h * p.x.s[1] + t * p.x.s[2];
+  const int d0 = grp * p.g;
+  float amax = 0.0f;
+  for (int i = 0; i < p.g; ++i) {
+    amax = fmaxf(amax, fabsf(load_float(p.x.data, p.x.dtype, xrow + (d0 + i) * p.x.s[3])));
+  }
+  const float scale = fmaxf(amax / 7.0f, 1.0e-8f);
+
+  uint8_t* dst = p.packed + b * p.ps[0] + h * p.ps[1] + pos * p.ps[2];
+  for (int i = 0; i < p.g; i += 2) {
+    const float v0 = load_float(p.x.data, p.x.dtype, xrow + (d0 + i) * p.x.s[3]);
+    const float v1 = load_float(p.x.data, p.x.dtype, xrow + (d0 + i + 1) * p.x.s[3]);
+    int q0 = (int)rintf(v0 / scale);
+    int q1 = (int)rintf(v1 / scale);
+    q0 = min(max(q0, -8), 7);
+    q1 = min(max(q1, -8), 7);
+    dst[((d0 + i) >> 1) * p.ps[3]] = (uint8_t)(((q1 & 15) << 4) | (q0 & 15));
+  }
+  p.scale[b * p.ss[0] + h * p.ss[1] + pos * p.ss[2] + grp * p.ss[3]] = scale;
+}
+
+}  // namespace lq
+
+using namespace lq;
+
+extern "C" int lq_int4_pack_kv(const lq_tensor* x, const lq_tensor* packed,
+                               const lq_tensor* scale, const lq_tensor* positions,
+                               int group_size, void* stream) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 4, true)) != LQ_OK) return rc;
+  if ((rc = check_tensor(packed, "packed", 4, false, LQ_U8)) != LQ_OK) return rc;
+  if ((rc = check_tensor(scale, "scale", 4, false, LQ_F32)) != LQ_OK) return rc;
+  if ((rc = check_tensor(positions, "positions", 1, false, LQ_I64)) != LQ_OK) return rc;
+  const int64_t B = x->shape[0], H = x->shape[1], T = x->shape[2], D = x->shape[3];
+  if (group_size <= 0 || group_size % 2 != 0) {
+    return fail(LQ_ERR_INVALID_ARG, "group_size=%d must be even for INT4 packing", group_size);
+  }
+  if (D % group_size != 0) {
+    return fail(LQ_ERR_INVALID_ARG, "head_dim=%lld must be divisible by group_size=%d",
+                (long long)D, group_size);
+  }
+  const int64_t cap = packed->shape[2];
+  if (packed->shape[0] != B || packed->shape[1] != H || packed->shape[3] != D / 2) {
+    return fail(LQ_ERR_INVALID_ARG, "packed must be [%lld, %lld, cap, %lld]", (long long)B,
+                (long long)H, (long long)(D / 2));
+  }
+  if (scale->shape[0] != B || scale->shape[1] != H || scale->shape[2] != cap ||
+      scale->shape[3] != D / group_size) {
+    return fail(LQ_ERR_INVALID_ARG, "scale must be [%lld, %lld, %lld, %lld]", (long long)B,
+                (long long)H, (long long)cap, (long long)(D / group_size));
+  }
+  if (positions->shape[0] != T) {
+    return fail(LQ_ERR_INVALID_ARG, "positions has %lld entries for q_len=%lld",
+                (long long)positions->shape[0], (long long)T);
+  }
+  if (B == 0 || H == 0 || T == 0 || D == 0) return LQ_OK;
+
+  PackParams p{};
+  p.x = make_view(x);
+  p.packed = (uint8_t*)packed->data;
+  p.scale = (float*)scale->data;
+  for (int i = 0; i < 4; ++i) {
+    p.ps[i] = packed->stride[i];
+    p.ss[i] = scale->stride[i];
+  }
+  p.positions = (const int64_t*)positions->data;
+  p.pos_stride = positions->stride[0];
+  p.B = (int)B;
+  p.H = (int)H;
+  p.T = (int)T;
+  p.D = (int)D;
+  p.g = group_size;
+  p.cap = cap;
+  const int64_t total = B * H * T * (D / group_size);
+  const int threads = 256;
+  const int64_t blocks = (total + threads - 1) / threads;
+  hipLaunchKernelGGL(int4_pack_kernel, dim3((unsigned)blocks), dim3(threads), 0,
+                     (hipStream_t)stream, p);
+  return check_launch("lq_int4_pack_kv");
+}

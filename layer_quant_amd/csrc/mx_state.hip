@@ -1,0 +1,673 @@
+// MX8 / MX4 Mamba2 recurrent state: fused selective-state update, block encoder, decoder.
+//
+// Replaces the reference's Triton kernels in hybrid_quant/mamba_state_8b_kernel.py:
+//   _state_update_requant_mx8_row_kernel (:33-222)              -> mx_update_kernel<8, .>
+//   _state_update_mx8_kernel + _requantize_mx4_kernel (:225-544) -> mx_update_kernel<4, .>
+//   _quantize_initial_state_mx (:547-572, torch)                 -> mx_encode_kernel<., RNE>
+//
+// Layout (reference MambaStateKernelCache, :19-25), per state row (b, h, p) of N values:
+//   q_state    int8  [N]     one byte per mantissa in both formats
+//   shared_exp uint8 [N/16]  biased exponent of each 16-value block (127 = 2^0)
+//   micro_exp  uint8 [N/2]   0/1 per pair of values
+// One lane owns one 16-value block: a 16-byte mantissa load, an 8-byte micro-exponent load and a
+// 1-byte exponent load, all coalesced across the wave; the row's N/16 lanes are adjacent, so
+// y = sum_n h'_n C_n is a shuffle reduction inside the row's lane group. The update is one pass:
+// the MX4 path does not round-trip an fp32 state through HBM as the reference does.
+//
+// Encode of a block (bit-exact with the torch formula):
+//   t = max(absmax / (2M), 1e-30)           IEEE fp32 division
+//   e = clamp(ceil(log2 t) + 127, 1, 254)    ceil of the correctly rounded fp32 log2, computed
+//                                            exactly from t's exponent and mantissa bits
+//   base = absmax == 0 ? 1 : 2^(e-127);  micro = pair_absmax > M*base
+//   qa = min(|v| / (base*2^micro), M)        as a product with the exact reciprocal
+//   level = rint(qa) | floor(qa + 0.5) | floor(qa) + (u < qa - floor(qa));  min(level, M)
+#include <math.h>
+
+#include "lq_common.h"
+
+namespace lq {
+
+struct MxState {
+  int8_t* q;
+  uint8_t* e;
+  uint8_t* mi;
+  int64_t qs[3], es[3], ms[3];  // strides of (b, h, p); the innermost dimension is contiguous
+};
+
+struct MxUpdateParams {
+  MxState st;
+  View x, dt, dtb, A, B, C, D, z, out, uni;
+  int Bn, H, P, N, ratio, bpr, vbpr;
+  int has_dtb, has_D, has_z, softplus, a_row_const;
+  uint32_t key;
+  uint64_t rng_offset;
+};
+
+struct MxCodecParams {
+  MxState st;
+  View v;    // float state [B, H, P, N] (encode input or decode output)
+  View uni;  // uniforms for LQ_ROUND_SR_UNIFORM
+  int Bn, H, P, N, bpr;
+  uint32_t key;
+  uint64_t rng_offset;
+};
+
+__device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// ceil(log2(t)) with log2 correctly rounded to fp32, for positive normal t (or +inf).
+// t = 2^E * (1 + j 2^-23): the result is E if j == 0 or if E + log2(1 + j 2^-23) rounds back to
+// E in fp32, which happens for 0 < j <= T; T = floor(2^(kk-1) ln 2) where 2^(kk-24) is half the
+// fp32 spacing at E (kk = floor(log2|E|), one less for negative powers of two; E = 0 -> T = 0).
+__device__ __forceinline__ int ceil_log2_exact(float t) {
+  const uint32_t bits = __float_as_uint(t);
+  const int E = (int)((bits >> 23) & 0xffu) - 127;
+  const uint32_t mant = bits & 0x7fffffu;
+  const int a = E < 0 ? -E : E;
+  const int am = a > 0 ? a : 1;
+  const int fl = 31 - __clz(am);
+  const bool pow2 = (am & (am - 1)) == 0;
+  const int kk = (E < 0 && pow2) ? fl - 1 : fl;
+  const uint32_t thr = (E == 0) ? 0u : (uint32_t)ldexpf(0.693147182f, kk - 1);
+  return mant == 0 ? E : (mant <= thr ? E : E + 1);
+}
+
+// Counter-based 16-bit uniforms of one 16-value block: element n of the state draws counter
+// c = rng_offset + row*N + n; pair c>>1 hashes to 32 bits, the even element takes the low half.
+__device__ __forceinline__ void block_uniforms(uint32_t key, uint64_t c0, float (&u)[16]) {
+  const uint64_t pc0 = c0 >> 1;
+  const uint32_t lo0 = (uint32_t)pc0;
+  const uint32_t hi0 = (uint32_t)(pc0 >> 32);
+  const uint32_t kh0 = lowbias32(hi0 ^ key);
+  const uint32_t kh1 = lowbias32((hi0 + 1u) ^ key);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t lo = lo0 + (uint32_t)k;
+    const uint32_t kh = lo < lo0 ? kh1 : kh0;
+    const uint32_t bits = lowbias32(lo ^ kh);
+    u[2 * k] = (float)(bits & 0xffffu) * (1.0f / 65536.0f);
+    u[2 * k + 1] = (float)(bits >> 16) * (1.0f / 65536.0f);
+  }
+}
+
+template <int FB, int RMODE>
+__device__ __forceinline__ void encode16(const float (&v)[16], const float (&u)[16],
+                                         uint32_t (&qw)[4], uint32_t (&mw)[2], uint32_t& eb_out) {
+#pragma clang fp contract(off)
+  constexpr float M = FB == 8 ? 63.0f : 7.0f;
+  float pa[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    pa[k] = fmaxf(fabsf(v[2 * k]), fabsf(v[2 * k + 1]));
+    amax = fmaxf(amax, pa[k]);
+  }
+  const float t = fmaxf(amax / (2.0f * M), 1.0e-30f);
+  const int eb = min(max(ceil_log2_exact(t) + 127, 1), 254);
+  const int ebase = (amax == 0.0f) ? 127 : eb;
+  const float thr = M * __uint_as_float((uint32_t)ebase << 23);
+  uint32_t qb[16];
+  uint32_t mb[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int mi = pa[k] > thr ? 1 : 0;
+    const int se = ebase + mi;
+    // exact reciprocal of the pair scale 2^(se-127): normal for se <= 253, the subnormal 2^-127
+    // for se = 254, and 0 for se = 255 (scale +inf; only reachable when absmax is +inf)
+    const float inv = se <= 253 ? __uint_as_float((uint32_t)(254 - se) << 23)
+                                : (se == 254 ? __uint_as_float(0x00400000u) : 0.0f);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float a = fabsf(v[2 * k + i]);
+      float qa = fminf(a * inv, M);
+      float lvl;
+      if constexpr (RMODE == LQ_ROUND_NEAREST_EVEN) {
+        lvl = rintf(qa);
+      } else if constexpr (RMODE == LQ_ROUND_HALF_UP) {
+        lvl = floorf(qa + 0.5f);
+      } else {
+        const float fl = floorf(qa);
+        lvl = fl + ((u[2 * k + i] < qa - fl) ? 1.0f : 0.0f);
+      }
+      lvl = fminf(lvl, M);
+      int qi = (int)lvl;
+      if (v[2 * k + i] < 0.0f) qi = -qi;
+      qb[2 * k + i] = (uint32_t)qi & 0xffu;
+    }
+    mb[k] = (uint32_t)mi;
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    qw[w] = qb[4 * w] | (qb[4 * w + 1] << 8) | (qb[4 * w + 2] << 16) | (qb[4 * w + 3] << 24);
+  }
+  mw[0] = mb[0] | (mb[1] << 8) | (mb[2] << 16) | (mb[3] << 24);
+  mw[1] = mb[4] | (mb[5] << 8) | (mb[6] << 16) | (mb[7] << 24);
+  eb_out = (uint32_t)eb;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load_block(const MxState& s, int64_t qo, int64_t mo, int64_t eo,
+                                           uint32_t (&qw)[4], uint32_t (&mw)[2], uint32_t& ev) {
+  if constexpr (VEC) {
+    const uint4 a = *(const uint4*)(s.q + qo);
+    const uint2 m = *(const uint2*)(s.mi + mo);
+    qw[0] = a.x;
+    qw[1] = a.y;
+    qw[2] = a.z;
+    qw[3] = a.w;
+    mw[0] = m.x;
+    mw[1] = m.y;
+  } else {
+    const uint8_t* qb = (const uint8_t*)(s.q + qo);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      qw[w] = qb[4 * w] | (qb[4 * w + 1] << 8) | (qb[4 * w + 2] << 16) | ((uint32_t)qb[4 * w + 3] << 24);
+    }
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint8_t* mb = s.mi + mo + 4 * w;
+      mw[w] = mb[0] | (mb[1] << 8) | (mb[2] << 16) | ((uint32_t)mb[3] << 24);
+    }
+  }
+  ev = s.e[eo];
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store_block(const MxState& s, int64_t qo, int64_t mo, int64_t eo,
+                                            const uint32_t (&qw)[4], const uint32_t (&mw)[2],
+                                            uint32_t ev) {
+  if constexpr (VEC) {
+    *(uint4*)(s.q + qo) = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+    *(uint2*)(s.mi + mo) = make_uint2(mw[0], mw[1]);
+  } else {
+    uint8_t* qb = (uint8_t*)(s.q + qo);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qb[i] = (uint8_t)(qw[i >> 2] >> (8 * (i & 3)));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s.mi[mo + i] = (uint8_t)(mw[i >> 2] >> (8 * (i & 3)));
+  }
+  s.e[eo] = (uint8_t)ev;
+}
+
+// h_n = q_n * 2^(e - 127 + micro_pair(n)); the scale is built from exponent bits
+// (e + micro = 255 gives +inf, as exp2(128) does in fp32).
+__device__ __forceinline__ void decode16(const uint32_t (&qw)[4], const uint32_t (&mw)[2],
+                                         uint32_t ev, float (&h)[16]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t mi = (mw[k >> 2] >> (8 * (k & 3))) & 0xffu;
+    const float sc = __uint_as_float((ev + mi) << 23);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int n = 2 * k + i;
+      const int qv = (int)(int8_t)(qw[n >> 2] >> (8 * (n & 3)));
+      h[n] = (float)qv * sc;
+    }
+  }
+}
+
+__device__ __forceinline__ void load16(const View& v, int64_t base, int64_t stride, float (&o)[16]) {
+  if (stride == 1 && v.dtype == LQ_BF16 && ((((uintptr_t)v.data) + base * 2) & 15) == 0) {
+    const uint4* p4 = (const uint4*)((const uint16_t*)v.data + base);
+    const uint4 a = p4[0];
+    const uint4 b = p4[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = load_float(v.data, v.dtype, base + i * stride);
+  }
+}
+
+template <int FB, int RMODE, bool VEC>
+__global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
+  const int64_t rows = (int64_t)p.Bn * p.H * p.P;
+  const int64_t total = rows * p.vbpr;
+  int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool in_range = gid < total;
+  if (!in_range) gid = total - 1;
+  const int64_t row = gid / p.vbpr;
+  const int blk = (int)(gid - row * p.vbpr);
+  const bool active = in_range && blk < p.bpr;
+  const int blkc = min(blk, p.bpr - 1);
+  const int pp = (int)(row % p.P);
+  const int64_t bh = row / p.P;
+  const int h = (int)(bh % p.H);
+  const int b = (int)(bh / p.H);
+
+  const int64_t qo = b * p.st.qs[0] + h * p.st.qs[1] + pp * p.st.qs[2] + blkc * 16;
+  const int64_t mo = b * p.st.ms[0] + h * p.st.ms[1] + pp * p.st.ms[2] + blkc * 8;
+  const int64_t eo = b * p.st.es[0] + h * p.st.es[1] + pp * p.st.es[2] + blkc;
+  uint32_t qw[4], mw[2], ev;
+  load_block<VEC>(p.st, qo, mo, eo, qw, mw, ev);
+  float hv[16];
+  decode16(qw, mw, ev, hv);
+
+  // per-row scalars (ms.py:134-139)
+  const float xv = load_float(p.x.data, p.x.dtype, b * p.x.s[0] + h * p.x.s[1] + pp * p.x.s[2]);
+  float dtv = load_float(p.dt.data, p.dt.dtype, b * p.dt.s[0] + h * p.dt.s[1] + pp * p.dt.s[2]);
+  if (p.has_dtb) dtv += load_float(p.dtb.data, p.dtb.dtype, h * p.dtb.s[0] + pp * p.dtb.s[1]);
+  if (p.softplus) dtv = dtv <= 20.0f ? logf(1.0f + expf(dtv)) : dtv;
+
+  const int grp = h / p.ratio;
+  const int n0 = blkc * 16;
+  float Bv[16], Cv[16];
+  load16(p.B, b * p.B.s[0] + grp * p.B.s[1] + n0 * p.B.s[2], p.B.s[2], Bv);
+  load16(p.C, b * p.C.s[0] + grp * p.C.s[1] + n0 * p.C.s[2], p.C.s[2], Cv);
+  const int64_t abase = h * p.A.s[0] + pp * p.A.s[1] + n0 * p.A.s[2];
+  const float dA_row =
+      p.a_row_const ? expf(load_float(p.A.data, p.A.dtype, abase) * dtv) : 0.0f;
+
+  // h' = h * exp(A dt) + (B dt) x ; y = sum h' C (ms.py:158-159)
+  float ypart = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float dA =
+        p.a_row_const ? dA_row : expf(load_float(p.A.data, p.A.dtype, abase + i * p.A.s[2]) * dtv);
+    hv[i] = hv[i] * dA + (Bv[i] * dtv) * xv;
+    ypart += hv[i] * Cv[i];
+  }
+  if (!active) ypart = 0.0f;
+  for (int o = p.vbpr >> 1; o > 0; o >>= 1) ypart += __shfl_xor(ypart, o, 64);
+  if (in_range && blk == 0) {
+    float y = ypart;
+    if (p.has_D) y += xv * load_float(p.D.data, p.D.dtype, h * p.D.s[0] + pp * p.D.s[1]);
+    if (p.has_z) y *= load_float(p.z.data, p.z.dtype, b * p.z.s[0] + h * p.z.s[1] + pp * p.z.s[2]);
+    store_float(p.out.data, p.out.dtype, b * p.out.s[0] + h * p.out.s[1] + pp * p.out.s[2], y);
+  }
+
+  // writeback encode (ms.py:168-222, 512-544)
+  float u[16];
+  if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
+    block_uniforms(p.key, p.rng_offset + (uint64_t)row * (uint64_t)p.N + (uint64_t)n0, u);
+  } else if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {
+    const int64_t ub = b * p.uni.s[0] + h * p.uni.s[1] + pp * p.uni.s[2] + n0 * p.uni.s[3];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) u[i] = ((const float*)p.uni.data)[ub + i * p.uni.s[3]];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) u[i] = 0.0f;
+  }
+  uint32_t eo_bits;
+  encode16<FB, RMODE>(hv, u, qw, mw, eo_bits);
+  if (active) store_block<VEC>(p.st, qo, mo, eo, qw, mw, eo_bits);
+}
+
+template <int FB, int RMODE, bool VEC>
+__global__ __launch_bounds__(256) void mx_encode_kernel(MxCodecParams p) {
+  const int64_t total = (int64_t)p.Bn * p.H * p.P * p.bpr;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= total) return;
+  const int64_t row = gid / p.bpr;
+  const int blk = (int)(gid - row * p.bpr);
+  const int pp = (int)(row % p.P);
+  const int64_t bh = row / p.P;
+  const int h = (int)(bh % p.H);
+  const int b = (int)(bh / p.H);
+  const int n0 = blk * 16;
+  float v[16];
+  const int64_t vb = b * p.v.s[0] + h * p.v.s[1] + pp * p.v.s[2] + n0 * p.v.s[3];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = load_float(p.v.data, p.v.dtype, vb + i * p.v.s[3]);
+  float u[16];
+  if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
+    block_uniforms(p.key, p.rng_offset + (uint64_t)row * (uint64_t)p.N + (uint64_t)n0, u);
+  } else if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {
+    const int64_t ub = b * p.uni.s[0] + h * p.uni.s[1] + pp * p.uni.s[2] + n0 * p.uni.s[3];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) u[i] = ((const float*)p.uni.data)[ub + i * p.uni.s[3]];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) u[i] = 0.0f;
+  }
+  uint32_t qw[4], mw[2], eb;
+  encode16<FB, RMODE>(v, u, qw, mw, eb);
+  const int64_t qo = b * p.st.qs[0] + h * p.st.qs[1] + pp * p.st.qs[2] + n0;
+  const int64_t mo = b * p.st.ms[0] + h * p.st.ms[1] + pp * p.st.ms[2] + blk * 8;
+  const int64_t eo = b * p.st.es[0] + h * p.st.es[1] + pp * p.st.es[2] + blk;
+  store_block<VEC>(p.st, qo, mo, eo, qw, mw, eb);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void mx_decode_kernel(MxCodecParams p) {
+  const int64_t total = (int64_t)p.Bn * p.H * p.P * p.bpr;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= total) return;
+  const int64_t row = gid / p.bpr;
+  const int blk = (int)(gid - row * p.bpr);
+  const int pp = (int)(row % p.P);
+  const int64_t bh = row / p.P;
+  const int h = (int)(bh % p.H);
+  const int b = (int)(bh / p.H);
+  const int n0 = blk * 16;
+  const int64_t qo = b * p.st.qs[0] + h * p.st.qs[1] + pp * p.st.qs[2] + n0;
+  const int64_t mo = b * p.st.ms[0] + h * p.st.ms[1] + pp * p.st.ms[2] + blk * 8;
+  const int64_t eo = b * p.st.es[0] + h * p.st.es[1] + pp * p.st.es[2] + blk;
+  uint32_t qw[4], mw[2], ev;
+  load_block<VEC>(p.st, qo, mo, eo, qw, mw, ev);
+  float hv[16];
+  decode16(qw, mw, ev, hv);
+  const int64_t vb = b * p.v.s[0] + h * p.v.s[1] + pp * p.v.s[2] + n0 * p.v.s[3];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) store_float(p.v.data, p.v.dtype, vb + i * p.v.s[3], hv[i]);
+}
+
+// ---------------------------------------------------------------------------------------------
+// host
+// ---------------------------------------------------------------------------------------------
+static uint32_t lowbias32_host(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// Per-seed key of the counter generator: K = lowbias32(seed_lo ^ lowbias32(seed_hi ^ 0x9E3779B9)).
+static uint32_t seed_key(uint64_t seed) {
+  return lowbias32_host((uint32_t)seed ^ lowbias32_host((uint32_t)(seed >> 32) ^ 0x9E3779B9u));
+}
+
+static int check_state(const lq_tensor* q, const lq_tensor* e, const lq_tensor* m, int64_t& Bn,
+                       int64_t& H, int64_t& P, int64_t& N, MxState& st, bool& vec) {
+  int rc;
+  if ((rc = check_tensor(q, "q_state", 4, false, LQ_I8)) != LQ_OK) return rc;
+  if ((rc = check_tensor(e, "shared_exp", 4, false, LQ_U8)) != LQ_OK) return rc;
+  if ((rc = check_tensor(m, "micro_exp", 4, false, LQ_U8)) != LQ_OK) return rc;
+  Bn = q->shape[0];
+  H = q->shape[1];
+  P = q->shape[2];
+  N = q->shape[3];
+  if (N % 16 != 0) {
+    return fail(LQ_ERR_INVALID_ARG, "MX state dim must be divisible by 16, got %lld", (long long)N);
+  }
+  if (N / 16 > 64) {
+    return fail(LQ_ERR_UNSUPPORTED, "MX state dim %lld exceeds 1024", (long long)N);
+  }
+  const int64_t want_e[4] = {Bn, H, P, N / 16};
+  const int64_t want_m[4] = {Bn, H, P, N / 2};
+  for (int i = 0; i < 4; ++i) {
+    if (e->shape[i] != want_e[i]) {
+      return fail(LQ_ERR_INVALID_ARG, "shared_exp must be [B, H, P, N/16]");
+    }
+    if (m->shape[i] != want_m[i]) {
+      return fail(LQ_ERR_INVALID_ARG, "micro_exp must be [B, H, P, N/2]");
+    }
+  }
+  if (q->stride[3] != 1 || e->stride[3] != 1 || m->stride[3] != 1) {
+    return fail(LQ_ERR_INVALID_ARG, "MX state tensors need a contiguous last dimension");
+  }
+  st.q = (int8_t*)q->data;
+  st.e = (uint8_t*)e->data;
+  st.mi = (uint8_t*)m->data;
+  vec = (((uintptr_t)st.q & 15) == 0) && (((uintptr_t)st.mi & 7) == 0);
+  for (int i = 0; i < 3; ++i) {
+    st.qs[i] = q->stride[i];
+    st.es[i] = e->stride[i];
+    st.ms[i] = m->stride[i];
+    vec = vec && (st.qs[i] % 16 == 0) && (st.ms[i] % 8 == 0);
+  }
+  return LQ_OK;
+}
+
+static int check_round(int format_bits, int round_mode, const lq_tensor* uniform, int64_t Bn,
+                       int64_t H, int64_t P, int64_t N, uint64_t rng_offset) {
+  if (format_bits != 8 && format_bits != 4) {
+    return fail(LQ_ERR_INVALID_ARG, "Unsupported MX state format_bits=%d", format_bits);
+  }
+  if (round_mode < LQ_ROUND_NEAREST_EVEN || round_mode > LQ_ROUND_SR_COUNTER) {
+    return fail(LQ_ERR_INVALID_ARG, "unknown round_mode %d", round_mode);
+  }
+  if (round_mode == LQ_ROUND_SR_UNIFORM) {
+    int rc;
+    if ((rc = check_tensor(uniform, "uniform", 4, false, LQ_F32)) != LQ_OK) return rc;
+    const int64_t want[4] = {Bn, H, P, N};
+    for (int i = 0; i < 4; ++i) {
+      if (uniform->shape[i] != want[i]) {
+        return fail(LQ_ERR_INVALID_ARG, "uniform must be [B, H, P, N]");
+      }
+    }
+  }
+  if (round_mode == LQ_ROUND_SR_COUNTER && (rng_offset & 1u) != 0) {
+    return fail(LQ_ERR_INVALID_ARG, "rng_offset must be even");
+  }
+  return LQ_OK;
+}
+
+static int check_shape3(const lq_tensor* t, const char* name, int64_t a, int64_t b, int64_t c,
+                        bool allow_null) {
+  if (t == nullptr && allow_null) return LQ_OK;
+  int rc;
+  if ((rc = check_tensor(t, name, 3, true)) != LQ_OK) return rc;
+  if (t->shape[0] != a || t->shape[1] != b || t->shape[2] != c) {
+    return fail(LQ_ERR_INVALID_ARG, "Expected %s shape (%lld, %lld, %lld), got (%lld, %lld, %lld)",
+                name, (long long)a, (long long)b, (long long)c, (long long)t->shape[0],
+                (long long)t->shape[1], (long long)t->shape[2]);
+  }
+  return LQ_OK;
+}
+
+static int check_shape2(const lq_tensor* t, const char* name, int64_t a, int64_t b) {
+  if (t == nullptr) return LQ_OK;
+  int rc;
+  if ((rc = check_tensor(t, name, 2, true)) != LQ_OK) return rc;
+  if (t->shape[0] != a || t->shape[1] != b) {
+    return fail(LQ_ERR_INVALID_ARG, "Expected %s shape (%lld, %lld)", name, (long long)a,
+                (long long)b);
+  }
+  return LQ_OK;
+}
+
+template <int FB, int RMODE>
+static void launch_update(const MxUpdateParams& p, bool vec, dim3 grid, hipStream_t st) {
+  if (vec) {
+    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, true>), grid, dim3(256), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, false>), grid, dim3(256), 0, st, p);
+  }
+}
+
+template <int FB>
+static void dispatch_update(const MxUpdateParams& p, int rmode, bool vec, dim3 grid,
+                            hipStream_t st) {
+  switch (rmode) {
+    case LQ_ROUND_NEAREST_EVEN: launch_update<FB, LQ_ROUND_NEAREST_EVEN>(p, vec, grid, st); break;
+    case LQ_ROUND_HALF_UP: launch_update<FB, LQ_ROUND_HALF_UP>(p, vec, grid, st); break;
+    case LQ_ROUND_SR_UNIFORM: launch_update<FB, LQ_ROUND_SR_UNIFORM>(p, vec, grid, st); break;
+    default: launch_update<FB, LQ_ROUND_SR_COUNTER>(p, vec, grid, st); break;
+  }
+}
+
+template <int FB, int RMODE>
+static void launch_encode(const MxCodecParams& p, bool vec, dim3 grid, hipStream_t st) {
+  if (vec) {
+    hipLaunchKernelGGL((mx_encode_kernel<FB, RMODE, true>), grid, dim3(256), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((mx_encode_kernel<FB, RMODE, false>), grid, dim3(256), 0, st, p);
+  }
+}
+
+template <int FB>
+static void dispatch_encode(const MxCodecParams& p, int rmode, bool vec, dim3 grid,
+                            hipStream_t st) {
+  switch (rmode) {
+    case LQ_ROUND_NEAREST_EVEN: launch_encode<FB, LQ_ROUND_NEAREST_EVEN>(p, vec, grid, st); break;
+    case LQ_ROUND_HALF_UP: launch_encode<FB, LQ_ROUND_HALF_UP>(p, vec, grid, st); break;
+    case LQ_ROUND_SR_UNIFORM: launch_encode<FB, LQ_ROUND_SR_UNIFORM>(p, vec, grid, st); break;
+    default: launch_encode<FB, LQ_ROUND_SR_COUNTER>(p, vec, grid, st); break;
+  }
+}
+
+}  // namespace lq
+
+using namespace lq;
+
+extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* shared_exp,
+                                  const lq_tensor* micro_exp, const lq_tensor* x,
+                                  const lq_tensor* dt, const lq_tensor* dt_bias,
+                                  const lq_tensor* A, const lq_tensor* B, const lq_tensor* C,
+                                  const lq_tensor* D, const lq_tensor* z, const lq_tensor* out,
+                                  int format_bits, int dt_softplus, int round_mode,
+                                  const lq_tensor* uniform, uint64_t seed, uint64_t rng_offset,
+                                  void* stream) {
+  int rc;
+  int64_t Bn, H, P, N;
+  MxState st{};
+  bool vec = false;
+  if ((rc = check_state(q_state, shared_exp, micro_exp, Bn, H, P, N, st, vec)) != LQ_OK) return rc;
+  if ((rc = check_shape3(x, "x", Bn, H, P, false)) != LQ_OK) return rc;
+  if (B == nullptr || C == nullptr || B->ndim != 3 || C->ndim != 3) {
+    return fail(LQ_ERR_INVALID_ARG,
+                "Expected B and C with shape [batch, ngroups, dstate] for decode update.");
+  }
+  if ((rc = check_tensor(B, "B", 3, true)) != LQ_OK) return rc;
+  if ((rc = check_tensor(C, "C", 3, true)) != LQ_OK) return rc;
+  const int64_t G = B->shape[1];
+  if (B->shape[0] != Bn || B->shape[2] != N || C->shape[0] != Bn || C->shape[1] != G ||
+      C->shape[2] != N) {
+    return fail(LQ_ERR_INVALID_ARG,
+                "Expected B and C with shape [batch, ngroups, dstate] for decode update.");
+  }
+  if (G <= 0 || H % G != 0) {
+    return fail(LQ_ERR_INVALID_ARG, "nheads=%lld not divisible by ngroups=%lld", (long long)H,
+                (long long)G);
+  }
+  if ((rc = check_shape3(dt, "dt", Bn, H, P, false)) != LQ_OK) return rc;
+  if ((rc = check_shape3(z, "z", Bn, H, P, true)) != LQ_OK) return rc;
+  if ((rc = check_shape3(out, "out", Bn, H, P, false)) != LQ_OK) return rc;
+  if ((rc = check_shape2(dt_bias, "dt_bias", H, P)) != LQ_OK) return rc;
+  if ((rc = check_shape2(D, "D", H, P)) != LQ_OK) return rc;
+  if ((rc = check_tensor(A, "A", 3, true)) != LQ_OK) return rc;
+  if (A->shape[0] != H || A->shape[1] != P || A->shape[2] != N) {
+    return fail(LQ_ERR_INVALID_ARG, "Expected A shape (%lld, %lld, %lld)", (long long)H,
+                (long long)P, (long long)N);
+  }
+  if ((rc = check_round(format_bits, round_mode, uniform, Bn, H, P, N, rng_offset)) != LQ_OK) {
+    return rc;
+  }
+  if (Bn == 0 || H == 0 || P == 0) return LQ_OK;
+
+  MxUpdateParams p{};
+  p.st = st;
+  p.x = make_view(x);
+  p.dt = make_view(dt);
+  p.dtb = make_view(dt_bias);
+  p.A = make_view(A);
+  p.B = make_view(B);
+  p.C = make_view(C);
+  p.D = make_view(D);
+  p.z = make_view(z);
+  p.out = make_view(out);
+  p.uni = make_view(round_mode == LQ_ROUND_SR_UNIFORM ? uniform : nullptr);
+  p.Bn = (int)Bn;
+  p.H = (int)H;
+  p.P = (int)P;
+  p.N = (int)N;
+  p.ratio = (int)(H / G);
+  p.bpr = (int)(N / 16);
+  p.vbpr = 1;
+  while (p.vbpr < p.bpr) p.vbpr <<= 1;
+  p.has_dtb = dt_bias != nullptr;
+  p.has_D = D != nullptr;
+  p.has_z = z != nullptr;
+  p.softplus = dt_softplus != 0;
+  p.a_row_const = A->stride[2] == 0;
+  p.key = seed_key(seed);
+  p.rng_offset = rng_offset;
+
+  const int64_t lanes = Bn * H * P * p.vbpr;
+  const dim3 grid((unsigned)((lanes + 255) / 256));
+  hipStream_t s = (hipStream_t)stream;
+  if (format_bits == 8) {
+    dispatch_update<8>(p, round_mode, vec, grid, s);
+  } else {
+    dispatch_update<4>(p, round_mode, vec, grid, s);
+  }
+  return check_launch("lq_mx_state_update");
+}
+
+extern "C" int lq_mx_encode(const lq_tensor* state, const lq_tensor* q_state,
+                            const lq_tensor* shared_exp, const lq_tensor* micro_exp,
+                            int format_bits, int round_mode, const lq_tensor* uniform,
+                            uint64_t seed, uint64_t rng_offset, void* stream) {
+  int rc;
+  int64_t Bn, H, P, N;
+  MxState st{};
+  bool vec = false;
+  if ((rc = check_state(q_state, shared_exp, micro_exp, Bn, H, P, N, st, vec)) != LQ_OK) return rc;
+  if ((rc = check_tensor(state, "state", 4, true)) != LQ_OK) return rc;
+  for (int i = 0; i < 4; ++i) {
+    const int64_t want[4] = {Bn, H, P, N};
+    if (state->shape[i] != want[i]) {
+      return fail(LQ_ERR_INVALID_ARG, "state must match q_state [B, H, P, N]");
+    }
+  }
+  if ((rc = check_round(format_bits, round_mode, uniform, Bn, H, P, N, rng_offset)) != LQ_OK) {
+    return rc;
+  }
+  if (Bn == 0 || H == 0 || P == 0) return LQ_OK;
+  MxCodecParams p{};
+  p.st = st;
+  p.v = make_view(state);
+  p.uni = make_view(round_mode == LQ_ROUND_SR_UNIFORM ? uniform : nullptr);
+  p.Bn = (int)Bn;
+  p.H = (int)H;
+  p.P = (int)P;
+  p.N = (int)N;
+  p.bpr = (int)(N / 16);
+  p.key = seed_key(seed);
+  p.rng_offset = rng_offset;
+  const int64_t lanes = Bn * H * P * p.bpr;
+  const dim3 grid((unsigned)((lanes + 255) / 256));
+  hipStream_t s = (hipStream_t)stream;
+  if (format_bits == 8) {
+    dispatch_encode<8>(p, round_mode, vec, grid, s);
+  } else {
+    dispatch_encode<4>(p, round_mode, vec, grid, s);
+  }
+  return check_launch("lq_mx_encode");
+}
+
+extern "C" int lq_mx_decode(const lq_tensor* q_state, const lq_tensor* shared_exp,
+                            const lq_tensor* micro_exp, const lq_tensor* out, void* stream) {
+  int rc;
+  int64_t Bn, H, P, N;
+  MxState st{};
+  bool vec = false;
+  if ((rc = check_state(q_state, shared_exp, micro_exp, Bn, H, P, N, st, vec)) != LQ_OK) return rc;
+  if ((rc = check_tensor(out, "out", 4, true)) != LQ_OK) return rc;
+  for (int i = 0; i < 4; ++i) {
+    const int64_t want[4] = {Bn, H, P, N};
+    if (out->shape[i] != want[i]) {
+      return fail(LQ_ERR_INVALID_ARG, "out must match q_state [B, H, P, N]");
+    }
+  }
+  if (Bn == 0 || H == 0 || P == 0) return LQ_OK;
+  MxCodecParams p{};
+  p.st = st;
+  p.v = make_view(out);
+  p.Bn = (int)Bn;
+  p.H = (int)H;
+  p.P = (int)P;
+  p.N = (int)N;
+  p.bpr = (int)(N / 16);
+  const int64_t lanes = Bn * H * P * p.bpr;
+  const dim3 grid((unsigned)((lanes + 255) / 256));
+  if (vec) {
+    hipLaunchKernelGGL(mx_decode_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, p);
+  } else {
+    hipLaunchKernelGGL(mx_decode_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, p);
+  }
+  return check_launch("lq_mx_decode");
+}

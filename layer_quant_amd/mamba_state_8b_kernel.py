@@ -1,0 +1,234 @@
+"""MX8 / MX4 block-quantized Mamba2 recurrent state with a fused decode update.
+
+API-compatible with the reference module hybrid_quant/mamba_state_8b_kernel.py (cited as
+ms.py:line): same public names, argument meaning and error messages. The Triton kernels and the
+torch initial encoder are replaced by HIP kernels for gfx950 behind the C ABI
+(include/layer_quant.h):
+
+    _state_update_requant_mx8_row_kernel          -> lq_mx_state_update, format_bits 8 (ms.py:33-222)
+    _state_update_mx8_kernel + _requantize_mx4_kernel -> lq_mx_state_update, format_bits 4
+                                                     (ms.py:225-443, 494-544), one pass
+    _quantize_initial_state_mx (torch)            -> lq_mx_encode, nearest-even (ms.py:547-572)
+
+Stochastic rounding. The reference draws Triton's tl.rand per element at offset
+step*B*H*P*N + element index. This module keeps those offsets and, by default, draws from the
+library's counter-based generator (LQ_ROUND_SR_COUNTER, 16-bit uniforms from a hash of
+(seed, offset)). Passing `uniform=` (an fp32 tensor shaped like the state) rounds with those
+uniforms instead, for bit-exact comparison with any other implementation given the same tensor.
+`stochastic=False` selects the reference's deterministic floor(q + 0.5) writeback.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from types import SimpleNamespace
+
+import torch
+
+from . import _abi
+
+MX8_BLOCK_SIZE = 16
+MX8_PAIR_SIZE = 2
+MX8_MANTISSA_MAX = 63.0
+MX4_BLOCK_SIZE = 16
+MX4_PAIR_SIZE = 2
+MX4_MANTISSA_MAX = 7.0
+
+_MANTISSA_MAX = {8: MX8_MANTISSA_MAX, 4: MX4_MANTISSA_MAX}
+
+
+@dataclass
+class MambaStateKernelCache:
+    """MX state of one layer (ms.py:19-25): q_state int8 [B,H,P,N] (one byte per mantissa in
+    both formats), shared_exp uint8 [B,H,P,N/16], micro_exp uint8 [B,H,P,N/2], the format, and
+    the host-side step counter that offsets the stochastic-rounding stream."""
+
+    q_state: torch.Tensor
+    shared_exp: torch.Tensor
+    micro_exp: torch.Tensor
+    format_bits: int = 8
+    step: int = 0
+
+
+def _empty_mx_tensors(shape, device):
+    *lead, n = shape
+    return (torch.empty(shape, dtype=torch.int8, device=device),
+            torch.empty((*lead, n // MX8_BLOCK_SIZE), dtype=torch.uint8, device=device),
+            torch.empty((*lead, n // MX8_PAIR_SIZE), dtype=torch.uint8, device=device))
+
+
+def _quantize_initial_state_mx(state: torch.Tensor, *, format_bits: int, block_size: int,
+                               pair_size: int, mantissa_max: float):
+    """Nearest-even MX encode of a float state [..., N] (ms.py:547-572).
+
+    Runs lq_mx_encode on the state's GPU. The block and pair sizes and the mantissa maximum are
+    fixed by the format (16, 2 and 63 or 7); other values raise ValueError.
+    """
+    if state.shape[-1] % block_size != 0:
+        raise ValueError(
+            f"MX{format_bits} state dim must be divisible by {block_size}, got {state.shape[-1]}")
+    if (block_size, pair_size) != (MX8_BLOCK_SIZE, MX8_PAIR_SIZE) or \
+            _MANTISSA_MAX.get(format_bits) != float(mantissa_max):
+        raise ValueError(
+            f"MX{format_bits} kernels use 16-value blocks, pairs and mantissa max "
+            f"{_MANTISSA_MAX.get(format_bits)}; got block_size={block_size}, "
+            f"pair_size={pair_size}, mantissa_max={mantissa_max}")
+    lead = state.shape[:-1]
+    state4 = state.reshape(-1, 1, 1, state.shape[-1]) if state.dim() != 4 else state
+    q, e, m = _empty_mx_tensors(tuple(state4.shape), state.device)
+    _abi.mx_encode(state4, q, e, m, format_bits, _abi.ROUND_NEAREST_EVEN)
+    n = state.shape[-1]
+    return (q.reshape(*lead, n), e.reshape(*lead, n // block_size),
+            m.reshape(*lead, n // pair_size))
+
+
+def allocate_state_kernel_cache(ssm_state_4d: torch.Tensor, group_size: int = MX8_BLOCK_SIZE,
+                                format_bits: int = 8) -> MambaStateKernelCache:
+    """Encode a layer's state [B,H,P,N] into a new MX cache (ms.py:575-598)."""
+    if format_bits == 8:
+        if group_size != MX8_BLOCK_SIZE:
+            raise ValueError(
+                f"MX8 uses a fixed {MX8_BLOCK_SIZE}-value block, got group_size={group_size}")
+        q, e, m = _quantize_initial_state_mx(ssm_state_4d, format_bits=8,
+                                             block_size=MX8_BLOCK_SIZE, pair_size=MX8_PAIR_SIZE,
+                                             mantissa_max=MX8_MANTISSA_MAX)
+        return MambaStateKernelCache(q_state=q, shared_exp=e, micro_exp=m, format_bits=8)
+    if format_bits == 4:
+        if group_size != MX4_BLOCK_SIZE:
+            raise ValueError(
+                f"MX4 uses a fixed {MX4_BLOCK_SIZE}-value block, got group_size={group_size}")
+        q, e, m = _quantize_initial_state_mx(ssm_state_4d, format_bits=4,
+                                             block_size=MX4_BLOCK_SIZE, pair_size=MX4_PAIR_SIZE,
+                                             mantissa_max=MX4_MANTISSA_MAX)
+        return MambaStateKernelCache(q_state=q, shared_exp=e, micro_exp=m, format_bits=4)
+    raise ValueError(
+        f"Only MX8 and MX4 state quantization are supported, got format_bits={format_bits}")
+
+
+def dequantize_state_cache(cache: MambaStateKernelCache,
+                           dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Decoded state q * 2^(e - 127 + micro) [B,H,P,N] (no reference counterpart; the
+    reference decodes only inside its update kernels, ms.py:132, 322)."""
+    out = torch.empty(cache.q_state.shape, dtype=dtype, device=cache.q_state.device)
+    return _abi.mx_decode(cache.q_state, cache.shared_exp, cache.micro_exp, out)
+
+
+def _dt_bias_as_read(dt_bias: torch.Tensor | None, D: torch.Tensor | None, nheads: int,
+                     dim: int) -> torch.Tensor | None:
+    """The dt_bias values the reference kernels read: they index dt_bias with D's strides,
+    or with strides (0, 0) when D is None (ms.py:137, 335, 624)."""
+    if dt_bias is None:
+        return None
+    strides = tuple(D.stride()) if D is not None else (0, 0)
+    if tuple(dt_bias.shape) == (nheads, dim) and tuple(dt_bias.stride()) == strides:
+        return dt_bias
+    reach = dt_bias.storage_offset() + (nheads - 1) * max(strides[0], 0) + (dim - 1) * max(
+        strides[1], 0)
+    if reach >= dt_bias.untyped_storage().nbytes() // dt_bias.element_size():
+        raise ValueError(
+            "dt_bias read with D's strides would leave dt_bias's storage; pass dt_bias and D "
+            "with the same layout")
+    return dt_bias.as_strided((nheads, dim), strides)
+
+
+def mx_state_selective_update(cache: MambaStateKernelCache, x: torch.Tensor, dt: torch.Tensor,
+                              A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
+                              D: torch.Tensor | None = None, z: torch.Tensor | None = None,
+                              dt_bias: torch.Tensor | None = None, dt_softplus: bool = False,
+                              stochastic: bool = True, seed: int = 1234, *,
+                              uniform: torch.Tensor | None = None) -> torch.Tensor:
+    """One fused decode step on the MX state, in place; returns y [B,H,P] in x's dtype
+    (ms.py:601-721).
+
+    h = dequant(state); dt (+ dt_bias, read with D's strides); softplus if dt_softplus;
+    h' = h*exp(A*dt) + B*dt*x; y = sum_n h'*C (+ x*D) (* z); the state is re-encoded in its
+    format with stochastic rounding (counter generator or `uniform`) or, with
+    stochastic=False, floor(q + 0.5). cache.step advances by one.
+    """
+    if cache.q_state.ndim != 4:
+        raise ValueError(f"Expected q_state [B,H,P,N], got {tuple(cache.q_state.shape)}")
+    batch, nheads, dim, dstate = cache.q_state.shape
+    if x.shape != (batch, nheads, dim):
+        raise ValueError(f"Expected x shape {(batch, nheads, dim)}, got {tuple(x.shape)}")
+    if B.ndim != 3 or C.ndim != 3:
+        raise ValueError("Expected B and C with shape [batch, ngroups, dstate] for decode update.")
+    if cache.format_bits not in (8, 4):
+        raise ValueError(f"Unsupported MX state format_bits={cache.format_bits}")
+    out = torch.empty_like(x)
+    if not stochastic:
+        mode = _abi.ROUND_HALF_UP
+    elif uniform is not None:
+        mode = _abi.ROUND_SR_UNIFORM
+    else:
+        mode = _abi.ROUND_SR_COUNTER
+    rng_offset = cache.step * batch * nheads * dim * dstate
+    _abi.mx_state_update(cache.q_state, cache.shared_exp, cache.micro_exp, x, dt,
+                         _dt_bias_as_read(dt_bias, D, nheads, dim), A, B, C, D, z, out,
+                         cache.format_bits, dt_softplus, mode,
+                         uniform=uniform if mode == _abi.ROUND_SR_UNIFORM else None,
+                         seed=seed, rng_offset=rng_offset)
+    cache.step += 1
+    return out
+
+
+def mx8_state_selective_update(*args, **kwargs) -> torch.Tensor:
+    return mx_state_selective_update(*args, **kwargs)
+
+
+def mx4_state_selective_update(*args, **kwargs) -> torch.Tensor:
+    return mx_state_selective_update(*args, **kwargs)
+
+
+def patch_nemotron_h_mamba_decode_state_kernel(model, group_size: int = MX8_BLOCK_SIZE,
+                                               stochastic: bool = True, seed: int = 1234) -> None:
+    """Rebind the remote module's selective_state_update (ms.py:732-767).
+
+    States registered through register_mamba_state_kernel_caches (looked up by id) take the MX
+    update; any other state falls through to the original function. The rounding mode and seed
+    live on the module and may be changed by calling this again.
+    """
+    module = __import__(model.__class__.__module__, fromlist=["selective_state_update"])
+    original = getattr(module, "_mx_state_kernel_original", module.selective_state_update)
+    module._mx_state_kernel_stochastic = stochastic
+    module._mx_state_kernel_seed = seed
+
+    def selective_state_update_mx(ssm_state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
+                                  dt_softplus=False):
+        registry = getattr(module, "_mamba_decode_state_kernel_caches", {})
+        mx_cache = registry.get(id(ssm_state))
+        if mx_cache is None:
+            return original(ssm_state, x, dt, A, B, C, D=D, z=z, dt_bias=dt_bias,
+                            dt_softplus=dt_softplus)
+        return mx_state_selective_update(
+            mx_cache, x, dt, A, B, C, D=D, z=z, dt_bias=dt_bias, dt_softplus=dt_softplus,
+            stochastic=getattr(module, "_mx_state_kernel_stochastic", True),
+            seed=getattr(module, "_mx_state_kernel_seed", 1234))
+
+    if not getattr(module, "_mx_state_kernel_patched", False):
+        module.selective_state_update = selective_state_update_mx
+        module._mx_state_kernel_original = original
+        module._mx_state_kernel_patched = True
+    model._mx_state_kernel_group_size = group_size
+
+
+def register_mamba_state_kernel_caches(model, cache_params, mode_by_layer: dict[int, str]) -> None:
+    """Encode each listed layer's ssm_state into an MX cache keyed by id(ssm_state)
+    (ms.py:770-796); publishes the registry on the model and on the remote module."""
+    registry = {}
+    for layer_idx, mode in mode_by_layer.items():
+        if mode not in {"mx8", "mx4"}:
+            raise ValueError(f"Only MX8 and MX4 state caches are supported, got mode={mode!r}")
+        mixer = model.backbone.layers[layer_idx].mixer
+        ssm_state = cache_params.ssm_states[layer_idx]
+        state_4d = ssm_state.view(ssm_state.shape[0], mixer.num_heads, mixer.head_dim,
+                                  mixer.ssm_state_size)
+        bits = 8 if mode == "mx8" else 4
+        registry[id(ssm_state)] = allocate_state_kernel_cache(
+            state_4d, group_size=MX8_BLOCK_SIZE if bits == 8 else MX4_BLOCK_SIZE,
+            format_bits=bits)
+    model._mamba_decode_state_kernel_caches = registry
+    module = __import__(model.__class__.__module__, fromlist=["selective_state_update"])
+    module._mamba_decode_state_kernel_caches = dict(registry)
+    model._mamba_decode_state_kernel_meta = {
+        idx: SimpleNamespace(mode=mode, block_size=16, format_bits=8 if mode == "mx8" else 4)
+        for idx, mode in mode_by_layer.items()
+    }

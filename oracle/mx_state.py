@@ -1,0 +1,220 @@
+"""CPU restatement of the reference's MX8/MX4 Mamba2 state path -- TEST INFRASTRUCTURE ONLY.
+
+Reference: hybrid_quant/mamba_state_8b_kernel.py (cited as ms.py:line below).
+
+MX block format (ms.py:11-25): 16-value blocks along d_state; one biased 8-bit shared exponent
+per block (127 = 2^0); one micro-exponent bit per pair of values; signed integer mantissas
+|q| <= M with M = 63 (MX8) or 7 (MX4), stored one int8 per value in both formats.
+Encode of a block with absmax a (ms.py:168-203, 512-534, 557-571):
+    e     = clamp(ceil(log2(max(a / (2M), 1e-30))) + 127, 1, 254)
+    base  = 1 if a == 0 else 2^(e - 127)
+    micro = pair_absmax > M * base
+    qa    = min(|v| / (base * 2^micro), M)
+    level = round(qa)  (one of the modes below), min(level, M), negated when v < 0
+Rounding modes: nearest-even (torch.round, initial encode ms.py:568), half-up floor(qa + 0.5)
+(deterministic writeback ms.py:201, 482, 531), stochastic floor(qa) + (u < qa - floor(qa))
+(ms.py:196-199, 528-530) with u from a supplied tensor or from oracle.rng.
+
+ceil(log2(t)) is defined as the ceiling of the correctly rounded fp32 log2 of t. For a t with
+unbiased exponent E and mantissa field j, that ceiling is E when j == 0, E when the fp32 value
+of E + log2(1 + j*2^-23) rounds back to E, and E + 1 otherwise. The rounding back to E happens
+exactly for 0 < j <= T(E), where T depends only on the fp32 spacing around E and is tabulated
+below; torch's fp32 log2 agrees with it wherever it is correctly rounded.
+
+Pinning (tests/test_oracle_mx.py): the T table against a 60-digit mpmath evaluation for every
+reachable E; ceil_log2 against exact integer comparisons away from the rounding band; encode
+invariants (|q| <= M, e in [1, 254], micro in {0,1}); half-step error bound of the nearest-even
+decode; the all-zero block (e = 28, q = 0); exact powers of two; the floor(q + 0.5) double
+rounding case; stochastic rounding with u = 0 (ceil) and u -> 1 (floor) and its unbiasedness;
+the update's closed forms (dt = 0 leaves h unchanged so the writeback is a pure re-encode;
+A = 0 gives h + dt*B*x; softplus threshold at 20) against an independent float64 evaluation.
+bf16_state_update (drift baseline) restates mamba_ssm's selective_state_update, a dependency
+(mamba-ssm 2.3.2.post1) that is not installed: parity unpinned beyond the HF torch fallback it
+follows (transformers nemotron_h mamba2_selective_state_update).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import rng
+
+BLOCK = 16
+PAIR = 2
+MANTISSA_MAX = {8: 63.0, 4: 7.0}
+EXP_FLOOR = np.float32(1.0e-30)
+
+ROUND_NEAREST_EVEN = 0
+ROUND_HALF_UP = 1
+ROUND_SR_UNIFORM = 2
+ROUND_SR_COUNTER = 3
+
+# T(kk) for kk = -1..8, where the half spacing of fp32 around E is 2^(kk - 24).
+# T(kk) = largest j with log2(1 + j*2^-23) < 2^(kk-24)  (= floor(2^(kk-1) * ln 2) here).
+CEIL_LOG2_T = np.array([0, 0, 0, 1, 2, 5, 11, 22, 44, 88], dtype=np.int64)
+
+
+def _spacing_class(e: np.ndarray) -> np.ndarray:
+    """kk such that half the fp32 spacing at the value E + log2(1 + tiny) is 2^(kk - 24)."""
+    a = np.abs(e).astype(np.int64)
+    a_safe = np.maximum(a, 1)
+    fl = np.floor(np.log2(a_safe.astype(np.float64))).astype(np.int64)
+    # guard the float64 floor(log2) at exact powers of two
+    fl = np.where((np.int64(1) << (fl + 1)) <= a_safe, fl + 1, fl)
+    fl = np.where((np.int64(1) << fl) > a_safe, fl - 1, fl)
+    pow2 = (a_safe & (a_safe - 1)) == 0
+    return np.where((e < 0) & pow2, fl - 1, fl)
+
+
+def ceil_log2_f32(t: np.ndarray) -> np.ndarray:
+    """ceil(fp32 correctly rounded log2(t)) for positive normal (or +inf) float32 t."""
+    t = np.asarray(t, dtype=np.float32)
+    bits = t.view(np.uint32).astype(np.int64)
+    e = ((bits >> 23) & 0xFF) - 127
+    mant = bits & 0x7FFFFF
+    kk = _spacing_class(e)
+    thr = CEIL_LOG2_T[np.clip(kk + 1, 0, len(CEIL_LOG2_T) - 1)]
+    thr = np.where(e == 0, 0, thr)
+    return np.where(mant == 0, e, np.where(mant <= thr, e, e + 1)).astype(np.int64)
+
+
+def exp2_scale(biased: np.ndarray) -> np.ndarray:
+    """2^(biased - 127) as float32 built from the exponent bits (biased 255 -> +inf)."""
+    b = np.asarray(biased, dtype=np.uint32)
+    return (b << np.uint32(23)).view(np.float32)
+
+
+def mx_encode(state, format_bits: int, round_mode: int = ROUND_NEAREST_EVEN,
+              uniform: np.ndarray | None = None, seed: int = 0,
+              rng_offset: int = 0) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Encode a float state [..., N] -> (q int8 [..., N], shared_exp u8 [..., N/16],
+    micro_exp u8 [..., N/2])."""
+    if isinstance(state, torch.Tensor):
+        state = state.detach().float().cpu().numpy()
+    v = np.asarray(state, dtype=np.float32)
+    n = v.shape[-1]
+    if n % BLOCK != 0:
+        raise ValueError(f"MX{format_bits} state dim must be divisible by {BLOCK}, got {n}")
+    m = np.float32(MANTISSA_MAX[format_bits])
+    blocks = v.reshape(*v.shape[:-1], n // BLOCK, BLOCK)
+    amax = np.abs(blocks).max(axis=-1)
+    t = np.maximum(amax / np.float32(2.0 * MANTISSA_MAX[format_bits]), EXP_FLOOR)
+    raw = ceil_log2_f32(t)
+    biased = np.clip(raw + 127, 1, 254)
+    base = np.where(amax == 0, np.float32(1.0), exp2_scale(biased)).astype(np.float32)
+    pairs = blocks.reshape(*blocks.shape[:-1], BLOCK // PAIR, PAIR)
+    pair_amax = np.abs(pairs).max(axis=-1)
+    micro = pair_amax > (m * base)[..., None]
+    pair_scale = (base[..., None] * np.where(micro, np.float32(2.0), np.float32(1.0))).astype(
+        np.float32)
+    qa = np.minimum(np.abs(pairs) / pair_scale[..., None], m)
+    if round_mode == ROUND_NEAREST_EVEN:
+        level = np.rint(qa)
+    elif round_mode == ROUND_HALF_UP:
+        level = np.floor(qa + np.float32(0.5))
+    elif round_mode in (ROUND_SR_UNIFORM, ROUND_SR_COUNTER):
+        if round_mode == ROUND_SR_COUNTER:
+            u = rng.state_uniforms(seed, rng_offset, v.shape).reshape(pairs.shape)
+        else:
+            if uniform is None:
+                raise ValueError("ROUND_SR_UNIFORM needs a uniform tensor")
+            if isinstance(uniform, torch.Tensor):
+                uniform = uniform.detach().float().cpu().numpy()
+            u = np.asarray(uniform, dtype=np.float32).reshape(pairs.shape)
+        fl = np.floor(qa)
+        level = fl + (u < (qa - fl)).astype(np.float32)
+    else:
+        raise ValueError(f"unknown round_mode {round_mode}")
+    level = np.minimum(level, m)
+    q = np.where(pairs < 0, -level, level).reshape(v.shape).astype(np.int8)
+    shared = biased.astype(np.uint8)
+    micro_u8 = micro.astype(np.uint8).reshape(*v.shape[:-1], n // PAIR)
+    return q, shared, micro_u8
+
+
+def mx_decode(q, shared_exp, micro_exp) -> np.ndarray:
+    """h = q * 2^(e - 127 + micro) in float32 (ms.py:132, 322)."""
+    q = np.asarray(q.cpu().numpy() if isinstance(q, torch.Tensor) else q)
+    e = np.asarray(shared_exp.cpu().numpy() if isinstance(shared_exp, torch.Tensor) else shared_exp)
+    mi = np.asarray(micro_exp.cpu().numpy() if isinstance(micro_exp, torch.Tensor) else micro_exp)
+    n = q.shape[-1]
+    e_full = np.repeat(e.astype(np.uint32), BLOCK, axis=-1)
+    m_full = np.repeat(mi.astype(np.uint32), PAIR, axis=-1)
+    scale = exp2_scale(e_full + m_full)
+    assert scale.shape[-1] == n
+    return (q.astype(np.float32) * scale).astype(np.float32)
+
+
+def softplus_ref(x: torch.Tensor) -> torch.Tensor:
+    """ms.py:28-30: x <= 20 ? log(1 + exp(x)) : x."""
+    return torch.where(x <= 20.0, torch.log(1.0 + torch.exp(x)), x)
+
+
+def update_math(h: torch.Tensor, x, dt, A, B, C, D=None, z=None, dt_bias=None,
+                dt_softplus: bool = False, dtype=torch.float32):
+    """Dequantized-state update and output (ms.py:134-166, 324-368).
+
+    h [B,H,P,N]; x, dt [B,H,P]; A [H,P,N]; B, C [B,G,N]; D, dt_bias [H,P]; z [B,H,P].
+    Returns (h' [B,H,P,N], y [B,H,P]) computed in `dtype`.
+    """
+    bsz, nheads, dim, dstate = h.shape
+    ratio = nheads // B.shape[1]
+    hf = h.to(dtype)
+    xf = x.to(dtype)
+    dtf = dt.to(dtype)
+    if dt_bias is not None:
+        dtf = dtf + dt_bias.to(dtype)[None]
+    if dt_softplus:
+        dtf = softplus_ref(dtf)
+    grp = torch.arange(nheads) // ratio
+    Bh = B.to(dtype)[:, grp]  # [B,H,N]
+    Ch = C.to(dtype)[:, grp]
+    dA = torch.exp(A.to(dtype)[None] * dtf[..., None])
+    h2 = hf * dA + (Bh[:, :, None, :] * dtf[..., None]) * xf[..., None]
+    y = (h2 * Ch[:, :, None, :]).sum(dim=-1)
+    if D is not None:
+        y = y + xf * D.to(dtype)[None]
+    if z is not None:
+        y = y * z.to(dtype)
+    return h2, y
+
+
+def mx_update(q, shared_exp, micro_exp, x, dt, A, B, C, D=None, z=None, dt_bias=None,
+              dt_softplus: bool = False, format_bits: int = 8,
+              round_mode: int = ROUND_SR_COUNTER, uniform=None, seed: int = 1234,
+              rng_offset: int = 0):
+    """One fused MX update (ms.py:97-222 for MX8; :289-443 then :494-544 for MX4).
+
+    Returns (q', shared_exp', micro_exp', y f32, h' f32) with h' the fp32 updated state that
+    the writeback encodes.
+    """
+    h = torch.from_numpy(mx_decode(q, shared_exp, micro_exp))
+    h2, y = update_math(h, x.cpu(), dt.cpu(), A.cpu(), B.cpu(), C.cpu(),
+                        None if D is None else D.cpu(), None if z is None else z.cpu(),
+                        None if dt_bias is None else dt_bias.cpu(), dt_softplus)
+    q2, e2, m2 = mx_encode(h2.numpy(), format_bits, round_mode, uniform=uniform, seed=seed,
+                           rng_offset=rng_offset)
+    return q2, e2, m2, y, h2
+
+
+def bf16_state_update(state: torch.Tensor, x, dt, A, B, C, D=None, z=None, dt_bias=None,
+                      dt_softplus: bool = False):
+    """bf16-state baseline: fp32 update of a bf16 state, stored back as bf16 (round to nearest
+    even), y from the fp32 updated state; z gates with silu as mamba_ssm does.
+    Returns (new_state bf16, y f32)."""
+    h2, y_nogate = update_math(state.float(), x, dt, A, B, C, D, None, dt_bias, dt_softplus)
+    if z is not None:
+        zf = z.float()
+        y_nogate = y_nogate * (zf * torch.sigmoid(zf))
+    return h2.to(torch.bfloat16), y_nogate
+
+
+def update_algorithmic_bytes(batch: int, nheads: int, dim: int, dstate: int, ngroups: int,
+                             x_bytes: int = 2, out_bytes: int = 2, dt_bytes: int = 2) -> int:
+    """Unique bytes of one MX update call in the reference layout (state read + write once)."""
+    elems = batch * nheads * dim * dstate
+    state = 2 * (elems + elems // BLOCK + elems // PAIR)
+    io = batch * nheads * dim * (x_bytes + out_bytes)
+    bc = 2 * batch * ngroups * dstate * 2
+    scalars = batch * nheads * dt_bytes + 3 * nheads * 4
+    return state + io + bc + scalars

@@ -1,0 +1,29 @@
+import os
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The GPU device; skips only when this machine has no GPU at all (never hides a missing
+    library on a GPU machine: the kernels' loader raises in that case)."""
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU on this machine")
+    return torch.device("cuda:0")
+
+
+def pytest_runtest_setup(item):
+    if item.get_closest_marker("gpu") is not None:
+        print(f"\n[gpu-test] {item.nodeid}", flush=True)

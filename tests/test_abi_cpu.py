@@ -1,0 +1,124 @@
+"""The C ABI without a GPU: the library loads, exports every symbol include/*.h declares, and
+rejects invalid arguments before any HIP call."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from layer_quant_amd import _abi
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(lq_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _abi.lib()
+    declared = _declared_symbols()
+    assert declared, "no declarations found"
+    assert declared == set(_abi.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_version_and_empty_error():
+    assert _abi.abi_version() == 1
+    assert isinstance(_abi.last_error(), str)
+
+
+def _fake(shape, dtype, data=0x1000):
+    """A descriptor with a non-null fake device address (never dereferenced by validation)."""
+    t = _abi.LQTensor()
+    t.data = data
+    t.dtype = _abi.DTYPE_CODES[dtype]
+    t.ndim = len(shape)
+    stride = 1
+    for i in reversed(range(len(shape))):
+        t.shape[i] = shape[i]
+        t.stride[i] = stride
+        stride *= shape[i]
+    return ctypes.pointer(t)
+
+
+def test_pack_rejects_bad_arguments():
+    lib = _abi.lib()
+    x = _fake((2, 8, 1, 128), torch.bfloat16)
+    packed = _fake((2, 8, 16, 64), torch.uint8)
+    scale = _fake((2, 8, 16, 4), torch.float32)
+    pos = _fake((1,), torch.int64)
+    assert lib.lq_int4_pack_kv(None, packed, scale, pos, 32, None) == _abi.LQ_ERR_INVALID_ARG
+    assert lib.lq_int4_pack_kv(x, packed, scale, pos, 31, None) == _abi.LQ_ERR_INVALID_ARG
+    assert "even" in _abi.last_error()
+    assert lib.lq_int4_pack_kv(x, packed, scale, pos, 48, None) == _abi.LQ_ERR_INVALID_ARG
+    assert "divisible" in _abi.last_error()
+    bad_scale = _fake((2, 8, 16, 2), torch.float32)
+    assert lib.lq_int4_pack_kv(x, packed, bad_scale, pos, 32, None) == _abi.LQ_ERR_INVALID_ARG
+    two_pos = _fake((2,), torch.int64)
+    assert lib.lq_int4_pack_kv(x, packed, scale, two_pos, 32, None) == _abi.LQ_ERR_INVALID_ARG
+    assert "q_len" in _abi.last_error()
+
+
+def test_attention_rejects_bad_arguments():
+    lib = _abi.lib()
+    kp = _fake((2, 8, 64, 64), torch.uint8)
+    ks = _fake((2, 8, 64, 4), torch.float32)
+    out = _fake((2, 32, 128), torch.bfloat16)
+    q2 = _fake((2, 32, 2, 128), torch.bfloat16)
+    assert lib.lq_int4_decode_attention(q2, kp, kp, ks, ks, None, out, 10, 4, 32, None, 0,
+                                        None) == _abi.LQ_ERR_INVALID_ARG
+    assert "q_len=1" in _abi.last_error()
+    q = _fake((2, 32, 1, 128), torch.bfloat16)
+    assert lib.lq_int4_decode_attention(q, kp, kp, ks, ks, None, out, 65, 4, 32, None, 0,
+                                        None) == _abi.LQ_ERR_INVALID_ARG
+    assert lib.lq_int4_decode_attention(q, kp, kp, ks, ks, None, out, 10, 3, 32, None, 0,
+                                        None) == _abi.LQ_ERR_INVALID_ARG
+    # a long context needs split-K partials: no workspace is an error, not a fault
+    kp2 = _fake((2, 8, 16384, 64), torch.uint8)
+    ks2 = _fake((2, 8, 16384, 4), torch.float32)
+    assert _abi.int4_decode_attention_workspace(2, 32, 8, 128, 16384, 32) > 0
+    assert lib.lq_int4_decode_attention(q, kp2, kp2, ks2, ks2, None, out, 16384, 4, 32, None,
+                                        0, None) == _abi.LQ_ERR_WORKSPACE
+
+
+def test_mx_rejects_bad_arguments():
+    lib = _abi.lib()
+    qs = _fake((2, 4, 8, 128), torch.int8)
+    e = _fake((2, 4, 8, 8), torch.uint8)
+    m = _fake((2, 4, 8, 64), torch.uint8)
+    x = _fake((2, 4, 8), torch.bfloat16)
+    A = _fake((4, 8, 128), torch.float32)
+    B = _fake((2, 2, 128), torch.bfloat16)
+    out = _fake((2, 4, 8), torch.bfloat16)
+    args = [qs, e, m, x, x, None, A, B, B, None, None, out]
+    assert lib.lq_mx_state_update(*args, 6, 1, 1, None, 0, 0, None) == _abi.LQ_ERR_INVALID_ARG
+    assert "format_bits=6" in _abi.last_error()
+    assert lib.lq_mx_state_update(*args, 8, 1, 2, None, 0, 0, None) == _abi.LQ_ERR_INVALID_ARG
+    assert lib.lq_mx_state_update(*args, 8, 1, 3, None, 0, 1, None) == _abi.LQ_ERR_INVALID_ARG
+    assert "even" in _abi.last_error()
+    bad_x = _fake((2, 4, 7), torch.bfloat16)
+    args_bad = [qs, e, m, bad_x, x, None, A, B, B, None, None, out]
+    assert lib.lq_mx_state_update(*args_bad, 8, 1, 1, None, 0, 0, None) == _abi.LQ_ERR_INVALID_ARG
+    assert "Expected x shape" in _abi.last_error()
+    B2 = _fake((2, 128), torch.bfloat16)
+    args_b = [qs, e, m, x, x, None, A, B2, B, None, None, out]
+    assert lib.lq_mx_state_update(*args_b, 8, 1, 1, None, 0, 0, None) == _abi.LQ_ERR_INVALID_ARG
+    assert "[batch, ngroups, dstate]" in _abi.last_error()
+    q_odd = _fake((2, 4, 8, 40), torch.int8)
+    assert lib.lq_mx_encode(_fake((2, 4, 8, 40), torch.float32), q_odd, e, m, 8, 0, None, 0, 0,
+                            None) == _abi.LQ_ERR_INVALID_ARG
+    assert "divisible by 16" in _abi.last_error()
+
+
+def test_compute_wrappers_refuse_cpu_tensors():
+    x = torch.zeros(1, 1, 1, 128)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        _abi.int4_pack_kv(x, torch.zeros(1, 1, 4, 64, dtype=torch.uint8), torch.zeros(1, 1, 4, 4),
+                          torch.zeros(1, dtype=torch.long), 32)

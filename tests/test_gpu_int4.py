@@ -1,0 +1,192 @@
+"""GPU parity of the INT4 KV path through the C ABI: the pack is bit-exact against the oracle;
+attention (MFMA fast path and generic path) is within 2e-3 of the float64 oracle."""
+import pytest
+import torch
+
+from helpers import assert_close_rel
+from layer_quant_amd import _abi
+from hybrid_quant import int4_8b_attention as ia
+from oracle import int4_kv as oik
+
+pytestmark = pytest.mark.gpu
+
+
+def _activations(shape, seed, dtype=torch.bfloat16, outliers=True):
+    """~N(0,1) with about 1% of head_dim channels scaled by 8 (shared across tokens)."""
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=gen)
+    if outliers:
+        chan = torch.rand(shape[1], shape[-1], generator=gen) < 0.01
+        x = torch.where(chan[None, :, None, :] if x.dim() == 4 else chan[None], x * 8, x)
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("g", [16, 32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_pack_bit_exact(gpu, g, dtype):
+    b, h, t, d, cap = 3, 8, 5, 128, 32
+    x = _activations((b, h, t, d), 100 + g, dtype)
+    pos = torch.tensor([0, 7, 8, 31, 12])
+    packed = torch.full((b, h, cap, d // 2), 0xAB, dtype=torch.uint8, device=gpu)
+    scale = torch.full((b, h, cap, d // g), -1.0, device=gpu)
+    _abi.int4_pack_kv(x.to(gpu), packed, scale, pos.to(gpu), g)
+    torch.cuda.synchronize()
+    ref_p = torch.full((b, h, cap, d // 2), 0xAB, dtype=torch.uint8)
+    ref_s = torch.full((b, h, cap, d // g), -1.0)
+    oik.pack_into(ref_p, ref_s, x, pos, g)
+    assert torch.equal(packed.cpu(), ref_p)
+    assert torch.equal(scale.cpu(), ref_s)
+
+
+def test_pack_edge_values(gpu):
+    d, g = 128, 32
+    x = torch.zeros(1, 1, 4, d)
+    x[0, 0, 1, :8] = torch.tensor([7.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5])  # exact ties
+    x[0, 0, 2] = torch.randn(d) * 1e-30                                          # tiny values
+    x[0, 0, 3] = torch.randn(d) * 3e37                                           # huge values
+    pos = torch.arange(4)
+    packed = torch.zeros(1, 1, 4, d // 2, dtype=torch.uint8, device=gpu)
+    scale = torch.zeros(1, 1, 4, d // g, device=gpu)
+    _abi.int4_pack_kv(x.to(gpu), packed, scale, pos.to(gpu), g)
+    ref_p = torch.zeros(1, 1, 4, d // 2, dtype=torch.uint8)
+    ref_s = torch.zeros(1, 1, 4, d // g)
+    oik.pack_into(ref_p, ref_s, x, pos, g)
+    assert torch.equal(packed.cpu(), ref_p) and torch.equal(scale.cpu(), ref_s)
+    assert ref_s[0, 0, 0, 0].item() == torch.tensor(1e-8).item()
+
+
+def _packed_cache(b, hkv, s, d, g, seed, cap=None):
+    cap = cap or s
+    cache = oik.allocate_cache(b, hkv, cap, d, g)
+    k = _activations((b, hkv, s, d), seed, torch.bfloat16)
+    v = _activations((b, hkv, s, d), seed + 1, torch.bfloat16)
+    oik.pack_kv_into_cache(cache, k, v, torch.arange(s), g)
+    return cache
+
+
+def _run_attention(gpu, cache, q, s, nrep, g, mask=None, out_dtype=torch.float32):
+    dev = {k: v.to(gpu) for k, v in cache.items() if torch.is_tensor(v)}
+    out = torch.empty(q.shape[0], q.shape[1], q.shape[-1], dtype=out_dtype, device=gpu)
+    _abi.int4_decode_attention(q.to(gpu), dev["k_packed"], dev["v_packed"], dev["k_scale"],
+                               dev["v_scale"], None if mask is None else mask.to(gpu), out, s,
+                               nrep, g)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+ATTN_CASES = [
+    # b, hkv, nrep, s, g
+    (1, 8, 4, 1024, 32),   # the CPU reference config shape
+    (2, 8, 4, 1, 32),
+    (3, 2, 4, 37, 32),
+    (2, 4, 4, 1000, 64),
+    (2, 2, 4, 333, 128),
+    (2, 4, 2, 200, 32),
+    (1, 2, 1, 513, 32),
+    (2, 2, 8, 129, 64),
+    (1, 1, 16, 77, 128),
+    (2, 8, 4, 4133, 32),
+]
+
+
+@pytest.mark.parametrize("b,hkv,nrep,s,g", ATTN_CASES)
+def test_attention_parity_fast_and_generic(gpu, b, hkv, nrep, s, g):
+    d = 128
+    cache = _packed_cache(b, hkv, s, d, g, 200 + s, cap=s + 3)
+    q = _activations((b, hkv * nrep, 1, d), 300 + s, torch.bfloat16)
+    ref = oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
+                               cache["v_scale"], s, nrep, g)
+    fast = _run_attention(gpu, cache, q, s, nrep, g)            # bf16 q: MFMA path
+    generic = _run_attention(gpu, cache, q.float(), s, nrep, g)  # fp32 q: generic path
+    assert_close_rel(fast, ref, what="fast")
+    assert_close_rel(generic, ref, what="generic")
+
+
+@pytest.mark.parametrize("b,hkv,nrep,s,g,d", [(2, 2, 4, 300, 16, 128), (1, 4, 2, 150, 32, 64),
+                                              (2, 1, 3, 70, 64, 256)])
+def test_attention_generic_shapes(gpu, b, hkv, nrep, s, g, d):
+    cache = _packed_cache(b, hkv, s, d, g, 400 + d)
+    q = _activations((b, hkv * nrep, 1, d), 500 + d, torch.bfloat16)
+    ref = oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
+                               cache["v_scale"], s, nrep, g)
+    assert_close_rel(_run_attention(gpu, cache, q, s, nrep, g), ref)
+
+
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float32])
+def test_attention_masks(gpu, qdtype):
+    b, hkv, nrep, s, g, d = 3, 2, 4, 700, 32, 128
+    cache = _packed_cache(b, hkv, s, d, g, 600)
+    q = _activations((b, hkv * nrep, 1, d), 601).to(qdtype)
+    keep = torch.ones(b, s + 5, dtype=torch.bool)
+    keep[0, :100] = False          # left padding longer than a key tile
+    keep[1, 5:9] = False
+    keep[2, -300:-200] = False
+    mask = oik.decode_attention_mask(keep, b, s)
+    ref = oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
+                               cache["v_scale"], s, nrep, g, mask=mask)
+    assert_close_rel(_run_attention(gpu, cache, q, s, nrep, g, mask=mask), ref, what="keep")
+    bias = torch.randn(b, 1, 4, s) * 2
+    fmask = oik.decode_attention_mask(bias, b, s)
+    ref = oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
+                               cache["v_scale"], s, nrep, g, mask=fmask)
+    assert_close_rel(_run_attention(gpu, cache, q, s, nrep, g, mask=fmask), ref, what="bias")
+    short = torch.zeros(b, 1, 1, 450)  # keys at or beyond the mask length are excluded
+    ref = oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
+                               cache["v_scale"], s, nrep, g, mask=short)
+    assert_close_rel(_run_attention(gpu, cache, q, s, nrep, g, mask=short), ref, what="short")
+
+
+def test_attention_bf16_output(gpu):
+    b, hkv, nrep, s, g, d = 2, 8, 4, 2048, 32, 128
+    cache = _packed_cache(b, hkv, s, d, g, 700)
+    q = _activations((b, hkv * nrep, 1, d), 701)
+    ref = oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
+                               cache["v_scale"], s, nrep, g)
+    out = _run_attention(gpu, cache, q, s, nrep, g, out_dtype=torch.bfloat16)
+    assert_close_rel(out.float(), ref, rtol=8e-3, what="bf16 out")
+
+
+@pytest.mark.parametrize("b,s", [(64, 16384), (8, 4096)])
+def test_attention_full_size_sampled_heads(gpu, b, s):
+    """BASELINE sizes: random packed cache built on the GPU, oracle on sampled (b, kv head)."""
+    hkv, nrep, d, g = 8, 4, 128, 32
+    gen = torch.Generator(device=gpu).manual_seed(b + s)
+    kp = torch.randint(0, 256, (b, hkv, s, d // 2), dtype=torch.uint8, device=gpu, generator=gen)
+    vp = torch.randint(0, 256, (b, hkv, s, d // 2), dtype=torch.uint8, device=gpu, generator=gen)
+    ks = torch.rand(b, hkv, s, d // g, device=gpu, generator=gen) * 0.5 + 0.05
+    vs = torch.rand(b, hkv, s, d // g, device=gpu, generator=gen) * 0.5 + 0.05
+    q = (torch.randn(b, hkv * nrep, 1, d, device=gpu, generator=gen)).to(torch.bfloat16)
+    out = torch.empty(b, hkv * nrep, d, device=gpu)
+    _abi.int4_decode_attention(q, kp, vp, ks, vs, None, out, s, nrep, g)
+    torch.cuda.synchronize()
+    for bi, kv in [(0, 0), (b - 1, hkv - 1), (b // 2, 3)]:
+        sl = slice(bi, bi + 1)
+        ref = oik.decode_attention(q[sl, kv * nrep:(kv + 1) * nrep].cpu(),
+                                   kp[sl, kv:kv + 1].cpu(), vp[sl, kv:kv + 1].cpu(),
+                                   ks[sl, kv:kv + 1].cpu(), vs[sl, kv:kv + 1].cpu(), s, nrep, g)
+        assert_close_rel(out[sl, kv * nrep:(kv + 1) * nrep].cpu(), ref, what=f"b{bi} kv{kv}")
+
+
+def test_module_api_pack_then_attend(gpu):
+    """_ensure_layer_cache -> _pack_kv_into_cache -> _decode_attention, token by token."""
+    b, hkv, nrep, d, g, steps = 2, 8, 4, 128, 64, 40
+    holder = type("Cache", (), {})()
+    k_all = _activations((b, hkv, steps, d), 800)
+    v_all = _activations((b, hkv, steps, d), 801)
+    ref_cache = oik.allocate_cache(b, hkv, 64, d, g)
+    for t in range(steps):
+        cache = ia._ensure_layer_cache(holder, 0, b, hkv, t + 1, d, g, gpu)
+        pos = torch.tensor([t], device=gpu)
+        ia._pack_kv_into_cache(cache, k_all[:, :, t:t + 1].to(gpu), v_all[:, :, t:t + 1].to(gpu),
+                               pos, g)
+        oik.pack_kv_into_cache(ref_cache, k_all[:, :, t:t + 1], v_all[:, :, t:t + 1],
+                               torch.tensor([t]), g)
+    assert cache.length == steps and cache.k_packed.shape[2] == 64
+    assert torch.equal(cache.k_packed[:, :, :steps].cpu(), ref_cache["k_packed"][:, :, :steps])
+    assert torch.equal(cache.v_scale[:, :, :steps].cpu(), ref_cache["v_scale"][:, :, :steps])
+    q = _activations((b, hkv * nrep, 1, d), 802)
+    out = ia._decode_attention(q.to(gpu), cache, steps, nrep, g)
+    assert out.dtype == torch.bfloat16 and out.shape == (b, hkv * nrep, d)
+    ref = oik.decode_attention(q, ref_cache["k_packed"], ref_cache["v_packed"],
+                               ref_cache["k_scale"], ref_cache["v_scale"], steps, nrep, g)
+    assert_close_rel(out.float().cpu(), ref, rtol=8e-3)

@@ -1,0 +1,219 @@
+"""GPU parity of the MX8/MX4 state path through the C ABI: encoders and decoder bit-exact
+against the oracle in every rounding mode; the fused update's y within 2e-3, its writeback
+bit-exact when dt = 0 (h' = h) and within 2e-3 (normwise, with rare single-level boundary flips)
+otherwise; multi-step chains with the counter generator."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close_rel
+from layer_quant_amd import _abi
+from hybrid_quant import mamba_state_8b_kernel as ms
+from oracle import mx_state as omx
+
+pytestmark = pytest.mark.gpu
+
+
+def _state(shape, seed, dtype=torch.float32):
+    gen = torch.Generator().manual_seed(seed)
+    h = torch.randn(*shape, generator=gen) * 0.5
+    h = h * torch.exp(torch.randn(*shape[:-1], 1, generator=gen))  # per-row magnitudes
+    flat = h.view(-1, shape[-1])
+    flat[0, :16] = 0.0                                                 # an all-zero block
+    flat[1, :16] = 0.0
+    flat[1, 3] = 126 * 2.0 ** -7                                       # amax/126 a power of two
+    flat[2, 5] = np.float32(np.ldexp(1 + 2.0 ** -23, -3) * 126)        # inside the log2 band
+    flat[3, :16] *= 1e-20                                              # tiny block
+    return h.to(dtype)
+
+
+def _mx_tensors(shape, device):
+    b, h, p, n = shape
+    return (torch.empty(shape, dtype=torch.int8, device=device),
+            torch.empty(b, h, p, n // 16, dtype=torch.uint8, device=device),
+            torch.empty(b, h, p, n // 2, dtype=torch.uint8, device=device))
+
+
+def _assert_mx_equal(gpu_t, ref):
+    q, e, m = (t.cpu().numpy() for t in gpu_t)
+    rq, re_, rm = ref
+    assert np.array_equal(e, re_), f"exponents differ at {np.argwhere(e != re_)[:5]}"
+    assert np.array_equal(m, rm), f"micro bits differ at {np.argwhere(m != rm)[:5]}"
+    assert np.array_equal(q, rq), f"mantissas differ at {np.argwhere(q != rq)[:5]}"
+
+
+@pytest.mark.parametrize("fb", [8, 4])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_encode_bit_exact(gpu, fb, mode, dtype):
+    shape = (3, 8, 16, 128)
+    h = _state(shape, 10 + fb + mode, dtype)
+    uni = torch.rand(shape, generator=torch.Generator().manual_seed(5)) if mode == 2 else None
+    seed, off = 1234, 2 * 987654321
+    out = _mx_tensors(shape, gpu)
+    _abi.mx_encode(h.to(gpu), *out, fb, mode, None if uni is None else uni.to(gpu), seed, off)
+    ref = omx.mx_encode(h.float().numpy(), fb, mode, uniform=uni, seed=seed, rng_offset=off)
+    _assert_mx_equal(out, ref)
+
+
+@pytest.mark.parametrize("n", [128, 64, 48, 16])
+def test_encode_decode_state_widths(gpu, n):
+    shape = (2, 4, 8, n)
+    h = _state(shape, 20 + n)
+    out = _mx_tensors(shape, gpu)
+    _abi.mx_encode(h.to(gpu), *out, 8, 0)
+    ref = omx.mx_encode(h.numpy(), 8, 0)
+    _assert_mx_equal(out, ref)
+    deq = torch.empty(shape, device=gpu)
+    _abi.mx_decode(*out, deq)
+    assert np.array_equal(deq.cpu().numpy(), omx.mx_decode(*ref))
+
+
+def _inputs(bsz, nh, p_, n, ng, seed, device, dt_zero=False):
+    g = torch.Generator().manual_seed(seed)
+    t = dict(
+        x=torch.randn(bsz, nh, p_, generator=g).to(torch.bfloat16),
+        dt=torch.nn.functional.softplus(torch.randn(bsz, nh, p_, generator=g)).to(torch.bfloat16),
+        A=(-torch.exp(torch.rand(nh, generator=g) * 2))[:, None, None].expand(nh, p_, n),
+        B=torch.randn(bsz, ng, n, generator=g).to(torch.bfloat16),
+        C=torch.randn(bsz, ng, n, generator=g).to(torch.bfloat16),
+        D=torch.randn(nh, generator=g)[:, None].expand(nh, p_),
+        dt_bias=(torch.randn(nh, generator=g) * 0.1)[:, None].expand(nh, p_),
+    )
+    if dt_zero:
+        t["dt"] = torch.zeros_like(t["dt"])
+    return {k: v.to(device) for k, v in t.items()}
+
+
+def _cpu(t):
+    return {k: v.cpu() for k, v in t.items()}
+
+
+@pytest.mark.parametrize("fb", [8, 4])
+@pytest.mark.parametrize("mode", [1, 2, 3])
+def test_update_dt_zero_writeback_bit_exact(gpu, fb, mode):
+    shape = (2, 16, 8, 128)
+    h0 = _state(shape, 30 + fb)
+    q, e, m = omx.mx_encode(h0.numpy(), fb, 0)
+    t = _inputs(2, 16, 8, 128, 2, 31, gpu, dt_zero=True)
+    uni = torch.rand(shape, generator=torch.Generator().manual_seed(32))
+    st = [torch.from_numpy(a).to(gpu) for a in (q, e, m)]
+    out = torch.empty(2, 16, 8, device=gpu)
+    _abi.mx_state_update(*st, t["x"], t["dt"], None, t["A"], t["B"], t["C"], t["D"], None, out,
+                         fb, False, mode, uniform=uni.to(gpu) if mode == 2 else None, seed=99,
+                         rng_offset=4096)
+    c = _cpu(t)
+    rq, re_, rm, ry, rh = omx.mx_update(q, e, m, c["x"], c["dt"], c["A"], c["B"], c["C"],
+                                        D=c["D"], format_bits=fb, round_mode=mode, uniform=uni,
+                                        seed=99, rng_offset=4096)
+    assert torch.equal(rh, torch.from_numpy(omx.mx_decode(q, e, m)))  # dt = 0: h' = h
+    _assert_mx_equal(st, (rq, re_, rm))
+    assert_close_rel(out.cpu(), ry, what="y")
+
+
+@pytest.mark.parametrize("fb", [8, 4])
+@pytest.mark.parametrize("softplus", [True, False])
+def test_update_parity(gpu, fb, softplus):
+    bsz, nh, p_, n, ng = 4, 32, 16, 128, 4
+    shape = (bsz, nh, p_, n)
+    h0 = _state(shape, 40 + fb)
+    q, e, m = omx.mx_encode(h0.numpy(), fb, 0)
+    t = _inputs(bsz, nh, p_, n, ng, 41, gpu)
+    z = torch.randn(bsz, nh, p_, generator=torch.Generator().manual_seed(42)).to(gpu)
+    uni = torch.rand(shape, generator=torch.Generator().manual_seed(43))
+    st = [torch.from_numpy(a).to(gpu) for a in (q, e, m)]
+    out = torch.empty(bsz, nh, p_, device=gpu)
+    _abi.mx_state_update(*st, t["x"], t["dt"], t["dt_bias"], t["A"], t["B"], t["C"], t["D"], z,
+                         out, fb, softplus, 2, uniform=uni.to(gpu))
+    c = _cpu(t)
+    rq, re_, rm, ry, rh = omx.mx_update(q, e, m, c["x"], c["dt"], c["A"], c["B"], c["C"],
+                                        D=c["D"], z=z.cpu(), dt_bias=c["dt_bias"],
+                                        dt_softplus=softplus, format_bits=fb, round_mode=2,
+                                        uniform=uni)
+    assert_close_rel(out.cpu(), ry, what="y")
+    got = omx.mx_decode(*(a.cpu().numpy() for a in st))
+    want = omx.mx_decode(rq, re_, rm)
+    assert_close_rel(torch.from_numpy(got), torch.from_numpy(want), what="dequantized state")
+    same = np.mean(st[0].cpu().numpy() == rq)
+    assert same > 0.999, f"only {same:.5f} of mantissas bit-identical"
+
+
+def test_update_general_A_and_strides(gpu):
+    """A varying along d_state (per-element exp), fp32 inputs, non-contiguous x."""
+    bsz, nh, p_, n, ng = 2, 8, 8, 64, 2
+    shape = (bsz, nh, p_, n)
+    h0 = _state(shape, 50)
+    q, e, m = omx.mx_encode(h0.numpy(), 8, 0)
+    g = torch.Generator().manual_seed(51)
+    x = torch.randn(bsz, p_, nh, generator=g).transpose(1, 2)  # strided view
+    dt = torch.zeros(bsz, nh, p_)
+    A = -torch.rand(nh, p_, n, generator=g)
+    B = torch.randn(bsz, ng, n, generator=g)
+    C = torch.randn(bsz, ng, n, generator=g)
+    st = [torch.from_numpy(a).to(gpu) for a in (q, e, m)]
+    out = torch.empty(bsz, nh, p_, device=gpu)
+    _abi.mx_state_update(*st, x.to(gpu).transpose(1, 2).contiguous().transpose(1, 2), dt.to(gpu),
+                         None, A.to(gpu), B.to(gpu), C.to(gpu), None, None, out, 8, False, 1)
+    rq, re_, rm, ry, _ = omx.mx_update(q, e, m, x, dt, A, B, C, format_bits=8, round_mode=1)
+    _assert_mx_equal(st, (rq, re_, rm))
+    assert_close_rel(out.cpu(), ry, what="y")
+    dt = torch.rand(bsz, nh, p_, generator=g)
+    out2 = torch.empty(bsz, nh, p_, device=gpu)
+    _abi.mx_state_update(*st, x.to(gpu), dt.to(gpu), None, A.to(gpu), B.to(gpu), C.to(gpu), None,
+                         None, out2, 8, False, 1)
+    rq2, re2, rm2, ry2, _ = omx.mx_update(rq, re_, rm, x, dt, A, B, C, format_bits=8,
+                                          round_mode=1)
+    assert_close_rel(out2.cpu(), ry2, what="y (A per element)")
+
+
+@pytest.mark.parametrize("fb", [8, 4])
+def test_counter_chain_module_api(gpu, fb):
+    """allocate_state_kernel_cache + 5 chained updates with dt = 0 (pure re-encodes at rising
+    counter offsets) stay bit-exact with the oracle chain."""
+    shape = (2, 8, 4, 128)
+    h0 = _state(shape, 60 + fb, torch.bfloat16)
+    cache = ms.allocate_state_kernel_cache(h0.to(gpu), format_bits=fb)
+    ref = omx.mx_encode(h0.float().numpy(), fb, 0)
+    _assert_mx_equal((cache.q_state, cache.shared_exp, cache.micro_exp), ref)
+    t = _inputs(2, 8, 4, 128, 2, 61, gpu, dt_zero=True)
+    c = _cpu(t)
+    for step in range(5):
+        y = ms.mx_state_selective_update(cache, t["x"], t["dt"], t["A"], t["B"], t["C"],
+                                         D=t["D"], seed=77)
+        rq, re_, rm, ry, _ = omx.mx_update(*ref, c["x"], c["dt"], c["A"], c["B"], c["C"],
+                                           D=c["D"], format_bits=fb,
+                                           round_mode=omx.ROUND_SR_COUNTER, seed=77,
+                                           rng_offset=step * int(np.prod(shape)))
+        ref = (rq, re_, rm)
+        _assert_mx_equal((cache.q_state, cache.shared_exp, cache.micro_exp), ref)
+        assert y.dtype == torch.bfloat16
+        assert_close_rel(y.float().cpu(), ry, rtol=8e-3, what=f"y step {step}")
+    assert cache.step == 5
+    deq = ms.dequantize_state_cache(cache)
+    assert np.array_equal(deq.cpu().numpy(), omx.mx_decode(*ref))
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("fb", [4])
+def test_full_size_b64_dt_zero_bit_exact(gpu, fb):
+    """BASELINE size (B=64, 128 heads x 64 x 128): counter-generator writeback bit-exact.
+    (The numpy oracle needs about a minute here.)"""
+    shape = (64, 128, 64, 128)
+    gen = torch.Generator(device=gpu).manual_seed(70 + fb)
+    h0 = torch.randn(shape, device=gpu, generator=gen) * 0.5
+    st = _mx_tensors(shape, gpu)
+    _abi.mx_encode(h0, *st, fb, 0)
+    q0, e0, m0 = (a.cpu().numpy() for a in st)
+    x = torch.randn(64, 128, 64, device=gpu, generator=gen).to(torch.bfloat16)
+    dt = torch.zeros(64, 128, 64, device=gpu, dtype=torch.bfloat16)
+    A = (-torch.rand(128, device=gpu, generator=gen))[:, None, None].expand(128, 64, 128)
+    B = torch.randn(64, 8, 128, device=gpu, generator=gen).to(torch.bfloat16)
+    C = torch.randn(64, 8, 128, device=gpu, generator=gen).to(torch.bfloat16)
+    out = torch.empty(64, 128, 64, device=gpu, dtype=torch.bfloat16)
+    off = 3 * int(np.prod(shape))
+    _abi.mx_state_update(*st, x, dt, None, A, B, C, None, None, out, fb, False, 3, seed=1234,
+                         rng_offset=off)
+    torch.cuda.synchronize()
+    h = omx.mx_decode(q0, e0, m0)
+    ref = omx.mx_encode(h, fb, omx.ROUND_SR_COUNTER, seed=1234, rng_offset=off)
+    _assert_mx_equal(st, ref)
