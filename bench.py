@@ -47,6 +47,9 @@ def parse_args():
     ap.add_argument("--mamba-layers", type=int, default=24)
     ap.add_argument("--state-bits", type=int, default=4, choices=[4, 8])
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 1 GiB device-to-device copy, the reference kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     return ap.parse_args()
 
 
@@ -248,6 +251,13 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     log(f"building workload: batch {args.batch}, ctx {args.ctx}, {args.attn_layers} attention "
         f"+ {args.mamba_layers} MX{args.state_bits} layers")
     attn, mamba, sizes = build_workload(torch, args, dev)

@@ -20,7 +20,7 @@
 //                                            exactly from t's exponent and mantissa bits
 //   base = absmax == 0 ? 1 : 2^(e-127);  micro = pair_absmax > M*base
 //   qa = min(|v| / (base*2^micro), M)        as a product with the exact reciprocal
-//   level = rint(qa) | floor(qa + 0.5) | floor(qa) + (u < qa - floor(qa));  min(level, M)
+//   level = rint(qa) | floor(qa + 0.5) | floor(qa) + (u < qa - floor(qa))   (always <= M)
 #include <math.h>
 
 #include "lq_common.h"
@@ -37,7 +37,7 @@ struct MxState {
 struct MxUpdateParams {
   MxState st;
   View x, dt, dtb, A, B, C, D, z, out, uni;
-  int Bn, H, P, N, ratio, bpr, vbpr;
+  int Bn, H, P, N, ratio, bpr, vbpr_log2;
   int has_dtb, has_D, has_z, softplus, a_row_const;
   uint32_t key;
   uint64_t rng_offset;
@@ -47,10 +47,54 @@ struct MxCodecParams {
   MxState st;
   View v;    // float state [B, H, P, N] (encode input or decode output)
   View uni;  // uniforms for LQ_ROUND_SR_UNIFORM
-  int Bn, H, P, N, bpr;
+  int Bn, H, P, N, bpr, vbpr_log2;
   uint32_t key;
   uint64_t rng_offset;
 };
+
+// Grid (ceil(P * vbpr / 256), H, B): one lane per 16-value block of one (b, h) pair; the N/16
+// block lanes of a state row are adjacent (vbpr = N/16 rounded up to a power of two). Batch and
+// head come from the block index, so every per-(b, h) offset is uniform and lane offsets are
+// 32-bit.
+struct LaneIdx {
+  int b, h, pp, blk;
+  bool in_range, active;
+};
+
+__device__ __forceinline__ LaneIdx lane_index(int P, int vbpr_log2, int bpr) {
+  LaneIdx L;
+  L.h = blockIdx.y;
+  L.b = blockIdx.z;
+  const int lanes = P << vbpr_log2;
+  int idx = blockIdx.x * 256 + threadIdx.x;
+  L.in_range = idx < lanes;
+  if (!L.in_range) idx = lanes - 1;  // whole trailing row groups only; they store nothing
+  L.pp = idx >> vbpr_log2;
+  const int blk = idx & ((1 << vbpr_log2) - 1);
+  L.active = L.in_range && blk < bpr;
+  L.blk = min(blk, bpr - 1);
+  return L;
+}
+
+__device__ __forceinline__ int dtype_bytes(int dtype) {
+  return dtype == LQ_F32 ? 4 : 2;
+}
+
+// uniform base of a strided float view at (i0, i1) of its leading dimensions
+__device__ __forceinline__ const char* vbase(const View& v, int i0, int i1) {
+  return (const char*)v.data + ((int64_t)i0 * v.s[0] + (int64_t)i1 * v.s[1]) * dtype_bytes(v.dtype);
+}
+
+__device__ __forceinline__ float ldf(const char* base, int dtype, int idx) {
+  switch (dtype) {
+    case LQ_BF16:
+      return bf16_bits_to_float(((const uint16_t*)base)[idx]);
+    case LQ_F16:
+      return (float)(((const _Float16*)base)[idx]);
+    default:
+      return ((const float*)base)[idx];
+  }
+}
 
 __device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
   x ^= x >> 16;
@@ -78,26 +122,36 @@ __device__ __forceinline__ int ceil_log2_exact(float t) {
   return mant == 0 ? E : (mant <= thr ? E : E + 1);
 }
 
-// Counter-based 16-bit uniforms of one 16-value block: element n of the state draws counter
-// c = rng_offset + row*N + n; pair c>>1 hashes to 32 bits, the even element takes the low half.
-__device__ __forceinline__ void block_uniforms(uint32_t key, uint64_t c0, float (&u)[16]) {
+// Counter-based 16-bit uniforms of one 16-value block, returned as u * 2^16 (exact integers):
+// element n draws counter c = rng_offset + row*N + n; pair c>>1 hashes to 32 bits, the even
+// element takes the low half.
+__device__ __forceinline__ void block_uniforms(uint32_t key, uint64_t c0, float (&u16)[16]) {
   const uint64_t pc0 = c0 >> 1;
   const uint32_t lo0 = (uint32_t)pc0;
   const uint32_t hi0 = (uint32_t)(pc0 >> 32);
   const uint32_t kh0 = lowbias32(hi0 ^ key);
-  const uint32_t kh1 = lowbias32((hi0 + 1u) ^ key);
+  uint32_t kh[8];
+  if (__builtin_expect(lo0 > 0xfffffff8u, 0)) {  // the low word wraps inside this block
+    const uint32_t kh1 = lowbias32((hi0 + 1u) ^ key);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) kh[k] = (lo0 + (uint32_t)k < lo0) ? kh1 : kh0;
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) kh[k] = kh0;
+  }
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    const uint32_t lo = lo0 + (uint32_t)k;
-    const uint32_t kh = lo < lo0 ? kh1 : kh0;
-    const uint32_t bits = lowbias32(lo ^ kh);
-    u[2 * k] = (float)(bits & 0xffffu) * (1.0f / 65536.0f);
-    u[2 * k + 1] = (float)(bits >> 16) * (1.0f / 65536.0f);
+    const uint32_t bits = lowbias32((lo0 + (uint32_t)k) ^ kh[k]);
+    u16[2 * k] = (float)(bits & 0xffffu);
+    u16[2 * k + 1] = (float)(bits >> 16);
   }
 }
 
+// Encode 16 values. `u16` holds the stochastic-rounding uniforms scaled by 2^16 (so that the
+// comparison u < frac becomes u16 < frac * 2^16, both sides exact), unused otherwise.
+// The reference's final min(level, M) is omitted: every mode already yields level <= M.
 template <int FB, int RMODE>
-__device__ __forceinline__ void encode16(const float (&v)[16], const float (&u)[16],
+__device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16)[16],
                                          uint32_t (&qw)[4], uint32_t (&mw)[2], uint32_t& eb_out) {
 #pragma clang fp contract(off)
   constexpr float M = FB == 8 ? 63.0f : 7.0f;
@@ -112,7 +166,7 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u)[
   const int eb = min(max(ceil_log2_exact(t) + 127, 1), 254);
   const int ebase = (amax == 0.0f) ? 127 : eb;
   const float thr = M * __uint_as_float((uint32_t)ebase << 23);
-  uint32_t qb[16];
+  int qi[16];
   uint32_t mb[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -124,8 +178,7 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u)[
                                 : (se == 254 ? __uint_as_float(0x00400000u) : 0.0f);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const float a = fabsf(v[2 * k + i]);
-      float qa = fminf(a * inv, M);
+      const float qa = fminf(fabsf(v[2 * k + i]) * inv, M);
       float lvl;
       if constexpr (RMODE == LQ_ROUND_NEAREST_EVEN) {
         lvl = rintf(qa);
@@ -133,18 +186,18 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u)[
         lvl = floorf(qa + 0.5f);
       } else {
         const float fl = floorf(qa);
-        lvl = fl + ((u[2 * k + i] < qa - fl) ? 1.0f : 0.0f);
+        lvl = fl + ((u16[2 * k + i] < (qa - fl) * 65536.0f) ? 1.0f : 0.0f);
       }
-      lvl = fminf(lvl, M);
-      int qi = (int)lvl;
-      if (v[2 * k + i] < 0.0f) qi = -qi;
-      qb[2 * k + i] = (uint32_t)qi & 0xffu;
+      // sign of v (v < 0 -> negative level; -0.0 gives level 0 either way)
+      qi[2 * k + i] = (int)copysignf(lvl, v[2 * k + i]);
     }
     mb[k] = (uint32_t)mi;
   }
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    qw[w] = qb[4 * w] | (qb[4 * w + 1] << 8) | (qb[4 * w + 2] << 16) | (qb[4 * w + 3] << 24);
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)qi[4 * w + 1], (uint32_t)qi[4 * w], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)qi[4 * w + 3], (uint32_t)qi[4 * w + 2], 0x04000c0cu);
+    qw[w] = lo | hi;
   }
   mw[0] = mb[0] | (mb[1] << 8) | (mb[2] << 16) | (mb[3] << 24);
   mw[1] = mb[4] | (mb[5] << 8) | (mb[6] << 16) | (mb[7] << 24);
@@ -152,11 +205,11 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u)[
 }
 
 template <bool VEC>
-__device__ __forceinline__ void load_block(const MxState& s, int64_t qo, int64_t mo, int64_t eo,
+__device__ __forceinline__ void load_block(const int8_t* q, const uint8_t* mi, const uint8_t* e,
                                            uint32_t (&qw)[4], uint32_t (&mw)[2], uint32_t& ev) {
   if constexpr (VEC) {
-    const uint4 a = *(const uint4*)(s.q + qo);
-    const uint2 m = *(const uint2*)(s.mi + mo);
+    const uint4 a = *(const uint4*)q;
+    const uint2 m = *(const uint2*)mi;
     qw[0] = a.x;
     qw[1] = a.y;
     qw[2] = a.z;
@@ -164,45 +217,45 @@ __device__ __forceinline__ void load_block(const MxState& s, int64_t qo, int64_t
     mw[0] = m.x;
     mw[1] = m.y;
   } else {
-    const uint8_t* qb = (const uint8_t*)(s.q + qo);
+    const uint8_t* qb = (const uint8_t*)q;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       qw[w] = qb[4 * w] | (qb[4 * w + 1] << 8) | (qb[4 * w + 2] << 16) | ((uint32_t)qb[4 * w + 3] << 24);
     }
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
-      const uint8_t* mb = s.mi + mo + 4 * w;
-      mw[w] = mb[0] | (mb[1] << 8) | (mb[2] << 16) | ((uint32_t)mb[3] << 24);
+      mw[w] = mi[4 * w] | (mi[4 * w + 1] << 8) | (mi[4 * w + 2] << 16) | ((uint32_t)mi[4 * w + 3] << 24);
     }
   }
-  ev = s.e[eo];
+  ev = *e;
 }
 
 template <bool VEC>
-__device__ __forceinline__ void store_block(const MxState& s, int64_t qo, int64_t mo, int64_t eo,
+__device__ __forceinline__ void store_block(int8_t* q, uint8_t* mi, uint8_t* e,
                                             const uint32_t (&qw)[4], const uint32_t (&mw)[2],
                                             uint32_t ev) {
   if constexpr (VEC) {
-    *(uint4*)(s.q + qo) = make_uint4(qw[0], qw[1], qw[2], qw[3]);
-    *(uint2*)(s.mi + mo) = make_uint2(mw[0], mw[1]);
+    *(uint4*)q = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+    *(uint2*)mi = make_uint2(mw[0], mw[1]);
   } else {
-    uint8_t* qb = (uint8_t*)(s.q + qo);
+    uint8_t* qb = (uint8_t*)q;
 #pragma unroll
     for (int i = 0; i < 16; ++i) qb[i] = (uint8_t)(qw[i >> 2] >> (8 * (i & 3)));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s.mi[mo + i] = (uint8_t)(mw[i >> 2] >> (8 * (i & 3)));
+    for (int i = 0; i < 8; ++i) mi[i] = (uint8_t)(mw[i >> 2] >> (8 * (i & 3)));
   }
-  s.e[eo] = (uint8_t)ev;
+  *e = (uint8_t)ev;
 }
 
 // h_n = q_n * 2^(e - 127 + micro_pair(n)); the scale is built from exponent bits
 // (e + micro = 255 gives +inf, as exp2(128) does in fp32).
 __device__ __forceinline__ void decode16(const uint32_t (&qw)[4], const uint32_t (&mw)[2],
                                          uint32_t ev, float (&h)[16]) {
+  const uint32_t evs = ev << 23;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const uint32_t mi = (mw[k >> 2] >> (8 * (k & 3))) & 0xffu;
-    const float sc = __uint_as_float((ev + mi) << 23);
+    const float sc = __uint_as_float((mi << 23) + evs);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int n = 2 * k + i;
@@ -212,9 +265,13 @@ __device__ __forceinline__ void decode16(const uint32_t (&qw)[4], const uint32_t
   }
 }
 
-__device__ __forceinline__ void load16(const View& v, int64_t base, int64_t stride, float (&o)[16]) {
-  if (stride == 1 && v.dtype == LQ_BF16 && ((((uintptr_t)v.data) + base * 2) & 15) == 0) {
-    const uint4* p4 = (const uint4*)((const uint16_t*)v.data + base);
+// 16 consecutive d_state values of B or C: vector loads for contiguous bf16 (BCVEC), else
+// strided element loads of any float dtype.
+template <bool BCVEC>
+__device__ __forceinline__ void load16(const char* base, int dtype, int stride, int n0,
+                                       float (&o)[16]) {
+  if constexpr (BCVEC) {
+    const uint4* p4 = (const uint4*)((const uint16_t*)base + n0);
     const uint4 a = p4[0];
     const uint4 b = p4[1];
     const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -225,141 +282,139 @@ __device__ __forceinline__ void load16(const View& v, int64_t base, int64_t stri
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] = load_float(v.data, v.dtype, base + i * stride);
+    for (int i = 0; i < 16; ++i) o[i] = ldf(base, dtype, (n0 + i) * stride);
   }
 }
 
-template <int FB, int RMODE, bool VEC>
-__global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
-  const int64_t rows = (int64_t)p.Bn * p.H * p.P;
-  const int64_t total = rows * p.vbpr;
-  int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool in_range = gid < total;
-  if (!in_range) gid = total - 1;
-  const int64_t row = gid / p.vbpr;
-  const int blk = (int)(gid - row * p.vbpr);
-  const bool active = in_range && blk < p.bpr;
-  const int blkc = min(blk, p.bpr - 1);
-  const int pp = (int)(row % p.P);
-  const int64_t bh = row / p.P;
-  const int h = (int)(bh % p.H);
-  const int b = (int)(bh / p.H);
+template <int RMODE>
+__device__ __forceinline__ void block_u16(const View& uni, uint32_t key, uint64_t c0, int b, int h,
+                                          int pp, int n0, float (&u16)[16]) {
+  if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
+    block_uniforms(key, c0, u16);
+  } else if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {
+    const float* ub = (const float*)uni.data + ((int64_t)b * uni.s[0] + (int64_t)h * uni.s[1]);
+    const int off = pp * (int)uni.s[2] + n0 * (int)uni.s[3];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) u16[i] = ub[off + i * (int)uni.s[3]];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) u16[i] *= 65536.0f;  // exact: u * 2^16
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) u16[i] = 0.0f;
+  }
+}
 
-  const int64_t qo = b * p.st.qs[0] + h * p.st.qs[1] + pp * p.st.qs[2] + blkc * 16;
-  const int64_t mo = b * p.st.ms[0] + h * p.st.ms[1] + pp * p.st.ms[2] + blkc * 8;
-  const int64_t eo = b * p.st.es[0] + h * p.st.es[1] + pp * p.st.es[2] + blkc;
+template <int FB, int RMODE, bool VEC, bool BCVEC>
+__global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
+  const LaneIdx L = lane_index(p.P, p.vbpr_log2, p.bpr);
+  const int b = L.b, h = L.h, pp = L.pp;
+  const int n0 = L.blk * 16;
+
+  int8_t* qp = p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1] + pp * (int)p.st.qs[2] + n0;
+  uint8_t* mp = p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1] + pp * (int)p.st.ms[2] + L.blk * 8;
+  uint8_t* ep = p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1] + pp * (int)p.st.es[2] + L.blk;
   uint32_t qw[4], mw[2], ev;
-  load_block<VEC>(p.st, qo, mo, eo, qw, mw, ev);
+  load_block<VEC>(qp, mp, ep, qw, mw, ev);
   float hv[16];
   decode16(qw, mw, ev, hv);
 
   // per-row scalars (ms.py:134-139)
-  const float xv = load_float(p.x.data, p.x.dtype, b * p.x.s[0] + h * p.x.s[1] + pp * p.x.s[2]);
-  float dtv = load_float(p.dt.data, p.dt.dtype, b * p.dt.s[0] + h * p.dt.s[1] + pp * p.dt.s[2]);
-  if (p.has_dtb) dtv += load_float(p.dtb.data, p.dtb.dtype, h * p.dtb.s[0] + pp * p.dtb.s[1]);
+  const float xv = ldf(vbase(p.x, b, h), p.x.dtype, pp * (int)p.x.s[2]);
+  float dtv = ldf(vbase(p.dt, b, h), p.dt.dtype, pp * (int)p.dt.s[2]);
+  if (p.has_dtb) dtv += ldf(vbase(p.dtb, h, 0), p.dtb.dtype, pp * (int)p.dtb.s[1]);
   if (p.softplus) dtv = dtv <= 20.0f ? logf(1.0f + expf(dtv)) : dtv;
 
   const int grp = h / p.ratio;
-  const int n0 = blkc * 16;
   float Bv[16], Cv[16];
-  load16(p.B, b * p.B.s[0] + grp * p.B.s[1] + n0 * p.B.s[2], p.B.s[2], Bv);
-  load16(p.C, b * p.C.s[0] + grp * p.C.s[1] + n0 * p.C.s[2], p.C.s[2], Cv);
-  const int64_t abase = h * p.A.s[0] + pp * p.A.s[1] + n0 * p.A.s[2];
-  const float dA_row =
-      p.a_row_const ? expf(load_float(p.A.data, p.A.dtype, abase) * dtv) : 0.0f;
+  load16<BCVEC>(vbase(p.B, b, grp), p.B.dtype, (int)p.B.s[2], n0, Bv);
+  load16<BCVEC>(vbase(p.C, b, grp), p.C.dtype, (int)p.C.s[2], n0, Cv);
+  const char* ab = vbase(p.A, h, 0);
+  const int aoff = pp * (int)p.A.s[1] + n0 * (int)p.A.s[2];
+  const float dA_row = p.a_row_const ? expf(ldf(ab, p.A.dtype, aoff) * dtv) : 0.0f;
+  const float dtx = dtv * xv;
 
-  // h' = h * exp(A dt) + (B dt) x ; y = sum h' C (ms.py:158-159)
+  // h' = h * exp(A dt) + B dt x ; y = sum h' C (ms.py:158-159)
   float ypart = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const float dA =
-        p.a_row_const ? dA_row : expf(load_float(p.A.data, p.A.dtype, abase + i * p.A.s[2]) * dtv);
-    hv[i] = hv[i] * dA + (Bv[i] * dtv) * xv;
+    const float dA = p.a_row_const ? dA_row : expf(ldf(ab, p.A.dtype, aoff + i * (int)p.A.s[2]) * dtv);
+    hv[i] = hv[i] * dA + Bv[i] * dtx;
     ypart += hv[i] * Cv[i];
   }
-  if (!active) ypart = 0.0f;
-  for (int o = p.vbpr >> 1; o > 0; o >>= 1) ypart += __shfl_xor(ypart, o, 64);
-  if (in_range && blk == 0) {
+  if (!L.active) ypart = 0.0f;
+  for (int o = (1 << p.vbpr_log2) >> 1; o > 0; o >>= 1) ypart += __shfl_xor(ypart, o, 64);
+  if (L.in_range && L.blk == 0 && (threadIdx.x & ((1 << p.vbpr_log2) - 1)) == 0) {
     float y = ypart;
-    if (p.has_D) y += xv * load_float(p.D.data, p.D.dtype, h * p.D.s[0] + pp * p.D.s[1]);
-    if (p.has_z) y *= load_float(p.z.data, p.z.dtype, b * p.z.s[0] + h * p.z.s[1] + pp * p.z.s[2]);
-    store_float(p.out.data, p.out.dtype, b * p.out.s[0] + h * p.out.s[1] + pp * p.out.s[2], y);
+    if (p.has_D) y += xv * ldf(vbase(p.D, h, 0), p.D.dtype, pp * (int)p.D.s[1]);
+    if (p.has_z) y *= ldf(vbase(p.z, b, h), p.z.dtype, pp * (int)p.z.s[2]);
+    char* ob = (char*)vbase(p.out, b, h);
+    const int oi = pp * (int)p.out.s[2];
+    if (p.out.dtype == LQ_BF16) {
+      ((uint16_t*)ob)[oi] = float_to_bf16_bits(y);
+    } else if (p.out.dtype == LQ_F16) {
+      ((_Float16*)ob)[oi] = (_Float16)y;
+    } else {
+      ((float*)ob)[oi] = y;
+    }
   }
 
   // writeback encode (ms.py:168-222, 512-544)
-  float u[16];
-  if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
-    block_uniforms(p.key, p.rng_offset + (uint64_t)row * (uint64_t)p.N + (uint64_t)n0, u);
-  } else if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {
-    const int64_t ub = b * p.uni.s[0] + h * p.uni.s[1] + pp * p.uni.s[2] + n0 * p.uni.s[3];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) u[i] = ((const float*)p.uni.data)[ub + i * p.uni.s[3]];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) u[i] = 0.0f;
-  }
+  float u16[16];
+  const uint64_t row = ((uint64_t)b * p.H + h) * p.P + pp;
+  block_u16<RMODE>(p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0, b, h, pp, n0,
+                   u16);
   uint32_t eo_bits;
-  encode16<FB, RMODE>(hv, u, qw, mw, eo_bits);
-  if (active) store_block<VEC>(p.st, qo, mo, eo, qw, mw, eo_bits);
+  encode16<FB, RMODE>(hv, u16, qw, mw, eo_bits);
+  if (L.active) store_block<VEC>(qp, mp, ep, qw, mw, eo_bits);
 }
 
 template <int FB, int RMODE, bool VEC>
 __global__ __launch_bounds__(256) void mx_encode_kernel(MxCodecParams p) {
-  const int64_t total = (int64_t)p.Bn * p.H * p.P * p.bpr;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= total) return;
-  const int64_t row = gid / p.bpr;
-  const int blk = (int)(gid - row * p.bpr);
-  const int pp = (int)(row % p.P);
-  const int64_t bh = row / p.P;
-  const int h = (int)(bh % p.H);
-  const int b = (int)(bh / p.H);
-  const int n0 = blk * 16;
+  const LaneIdx L = lane_index(p.P, p.vbpr_log2, p.bpr);
+  if (!L.active) return;
+  const int b = L.b, h = L.h, pp = L.pp;
+  const int n0 = L.blk * 16;
   float v[16];
-  const int64_t vb = b * p.v.s[0] + h * p.v.s[1] + pp * p.v.s[2] + n0 * p.v.s[3];
+  const char* vb = vbase(p.v, b, h);
+  const int voff = pp * (int)p.v.s[2] + n0 * (int)p.v.s[3];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) v[i] = load_float(p.v.data, p.v.dtype, vb + i * p.v.s[3]);
-  float u[16];
-  if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
-    block_uniforms(p.key, p.rng_offset + (uint64_t)row * (uint64_t)p.N + (uint64_t)n0, u);
-  } else if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {
-    const int64_t ub = b * p.uni.s[0] + h * p.uni.s[1] + pp * p.uni.s[2] + n0 * p.uni.s[3];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) u[i] = ((const float*)p.uni.data)[ub + i * p.uni.s[3]];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) u[i] = 0.0f;
-  }
+  for (int i = 0; i < 16; ++i) v[i] = ldf(vb, p.v.dtype, voff + i * (int)p.v.s[3]);
+  float u16[16];
+  const uint64_t row = ((uint64_t)b * p.H + h) * p.P + pp;
+  block_u16<RMODE>(p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0, b, h, pp, n0,
+                   u16);
   uint32_t qw[4], mw[2], eb;
-  encode16<FB, RMODE>(v, u, qw, mw, eb);
-  const int64_t qo = b * p.st.qs[0] + h * p.st.qs[1] + pp * p.st.qs[2] + n0;
-  const int64_t mo = b * p.st.ms[0] + h * p.st.ms[1] + pp * p.st.ms[2] + blk * 8;
-  const int64_t eo = b * p.st.es[0] + h * p.st.es[1] + pp * p.st.es[2] + blk;
-  store_block<VEC>(p.st, qo, mo, eo, qw, mw, eb);
+  encode16<FB, RMODE>(v, u16, qw, mw, eb);
+  int8_t* qp = p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1] + pp * (int)p.st.qs[2] + n0;
+  uint8_t* mp = p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1] + pp * (int)p.st.ms[2] + L.blk * 8;
+  uint8_t* ep = p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1] + pp * (int)p.st.es[2] + L.blk;
+  store_block<VEC>(qp, mp, ep, qw, mw, eb);
 }
 
 template <bool VEC>
 __global__ __launch_bounds__(256) void mx_decode_kernel(MxCodecParams p) {
-  const int64_t total = (int64_t)p.Bn * p.H * p.P * p.bpr;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= total) return;
-  const int64_t row = gid / p.bpr;
-  const int blk = (int)(gid - row * p.bpr);
-  const int pp = (int)(row % p.P);
-  const int64_t bh = row / p.P;
-  const int h = (int)(bh % p.H);
-  const int b = (int)(bh / p.H);
-  const int n0 = blk * 16;
-  const int64_t qo = b * p.st.qs[0] + h * p.st.qs[1] + pp * p.st.qs[2] + n0;
-  const int64_t mo = b * p.st.ms[0] + h * p.st.ms[1] + pp * p.st.ms[2] + blk * 8;
-  const int64_t eo = b * p.st.es[0] + h * p.st.es[1] + pp * p.st.es[2] + blk;
+  const LaneIdx L = lane_index(p.P, p.vbpr_log2, p.bpr);
+  if (!L.active) return;
+  const int b = L.b, h = L.h, pp = L.pp;
+  const int n0 = L.blk * 16;
+  const int8_t* qp = p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1] + pp * (int)p.st.qs[2] + n0;
+  const uint8_t* mp = p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1] + pp * (int)p.st.ms[2] + L.blk * 8;
+  const uint8_t* ep = p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1] + pp * (int)p.st.es[2] + L.blk;
   uint32_t qw[4], mw[2], ev;
-  load_block<VEC>(p.st, qo, mo, eo, qw, mw, ev);
+  load_block<VEC>(qp, mp, ep, qw, mw, ev);
   float hv[16];
   decode16(qw, mw, ev, hv);
-  const int64_t vb = b * p.v.s[0] + h * p.v.s[1] + pp * p.v.s[2] + n0 * p.v.s[3];
+  char* ob = (char*)vbase(p.v, b, h);
+  const int off = pp * (int)p.v.s[2] + n0 * (int)p.v.s[3];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) store_float(p.v.data, p.v.dtype, vb + i * p.v.s[3], hv[i]);
+  for (int i = 0; i < 16; ++i) {
+    const int idx = off + i * (int)p.v.s[3];
+    if (p.v.dtype == LQ_BF16) {
+      ((uint16_t*)ob)[idx] = float_to_bf16_bits(hv[i]);
+    } else {
+      ((float*)ob)[idx] = hv[i];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -469,23 +524,54 @@ static int check_shape2(const lq_tensor* t, const char* name, int64_t a, int64_t
   return LQ_OK;
 }
 
+// Lane offsets below the (batch, head) level are 32-bit: the span of dims >= first must fit.
+static bool lane_span_ok(const lq_tensor* t, int first) {
+  if (t == nullptr) return true;
+  int64_t span = 0;
+  for (int i = 0; i < t->ndim; ++i) {
+    if (t->stride[i] < 0) return false;
+    if (i >= first && t->shape[i] > 0) span += (t->shape[i] - 1) * t->stride[i];
+  }
+  return span < ((int64_t)1 << 31) - 64;
+}
+
+static int log2_ceil(int v) {
+  int l = 0;
+  while ((1 << l) < v) ++l;
+  return l;
+}
+
+static bool bc_vector_ok(const lq_tensor* t) {
+  return t->dtype == LQ_BF16 && t->stride[2] == 1 && ((uintptr_t)t->data & 15) == 0 &&
+         t->stride[0] % 8 == 0 && t->stride[1] % 8 == 0;
+}
+
 template <int FB, int RMODE>
-static void launch_update(const MxUpdateParams& p, bool vec, dim3 grid, hipStream_t st) {
-  if (vec) {
-    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, true>), grid, dim3(256), 0, st, p);
+static void launch_update(const MxUpdateParams& p, bool vec, bool bcvec, dim3 grid,
+                          hipStream_t st) {
+  if (vec && bcvec) {
+    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, true, true>), grid, dim3(256), 0, st, p);
+  } else if (vec) {
+    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, true, false>), grid, dim3(256), 0, st, p);
+  } else if (bcvec) {
+    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, false, true>), grid, dim3(256), 0, st, p);
   } else {
-    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, false, false>), grid, dim3(256), 0, st, p);
   }
 }
 
 template <int FB>
-static void dispatch_update(const MxUpdateParams& p, int rmode, bool vec, dim3 grid,
+static void dispatch_update(const MxUpdateParams& p, int rmode, bool vec, bool bcvec, dim3 grid,
                             hipStream_t st) {
   switch (rmode) {
-    case LQ_ROUND_NEAREST_EVEN: launch_update<FB, LQ_ROUND_NEAREST_EVEN>(p, vec, grid, st); break;
-    case LQ_ROUND_HALF_UP: launch_update<FB, LQ_ROUND_HALF_UP>(p, vec, grid, st); break;
-    case LQ_ROUND_SR_UNIFORM: launch_update<FB, LQ_ROUND_SR_UNIFORM>(p, vec, grid, st); break;
-    default: launch_update<FB, LQ_ROUND_SR_COUNTER>(p, vec, grid, st); break;
+    case LQ_ROUND_NEAREST_EVEN:
+      launch_update<FB, LQ_ROUND_NEAREST_EVEN>(p, vec, bcvec, grid, st);
+      break;
+    case LQ_ROUND_HALF_UP: launch_update<FB, LQ_ROUND_HALF_UP>(p, vec, bcvec, grid, st); break;
+    case LQ_ROUND_SR_UNIFORM:
+      launch_update<FB, LQ_ROUND_SR_UNIFORM>(p, vec, bcvec, grid, st);
+      break;
+    default: launch_update<FB, LQ_ROUND_SR_COUNTER>(p, vec, bcvec, grid, st); break;
   }
 }
 
@@ -507,6 +593,19 @@ static void dispatch_encode(const MxCodecParams& p, int rmode, bool vec, dim3 gr
     case LQ_ROUND_SR_UNIFORM: launch_encode<FB, LQ_ROUND_SR_UNIFORM>(p, vec, grid, st); break;
     default: launch_encode<FB, LQ_ROUND_SR_COUNTER>(p, vec, grid, st); break;
   }
+}
+
+static int grid_for(int64_t Bn, int64_t H, int64_t P, int vbpr_log2, dim3& grid) {
+  if (Bn > 65535 || H > 65535) {
+    return fail(LQ_ERR_UNSUPPORTED, "batch %lld or heads %lld exceed 65535", (long long)Bn,
+                (long long)H);
+  }
+  const int64_t lanes = P << vbpr_log2;
+  if (lanes >= ((int64_t)1 << 31) - 256) {
+    return fail(LQ_ERR_UNSUPPORTED, "head_dim %lld too large", (long long)P);
+  }
+  grid = dim3((unsigned)((lanes + 255) / 256), (unsigned)H, (unsigned)Bn);
+  return LQ_OK;
 }
 
 }  // namespace lq
@@ -576,8 +675,7 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
   p.N = (int)N;
   p.ratio = (int)(H / G);
   p.bpr = (int)(N / 16);
-  p.vbpr = 1;
-  while (p.vbpr < p.bpr) p.vbpr <<= 1;
+  p.vbpr_log2 = log2_ceil(p.bpr);
   p.has_dtb = dt_bias != nullptr;
   p.has_D = D != nullptr;
   p.has_z = z != nullptr;
@@ -586,13 +684,21 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
   p.key = seed_key(seed);
   p.rng_offset = rng_offset;
 
-  const int64_t lanes = Bn * H * P * p.vbpr;
-  const dim3 grid((unsigned)((lanes + 255) / 256));
+  const lq_tensor* spans[] = {q_state, shared_exp, micro_exp, x, dt, B, C, z, out, uniform};
+  for (const lq_tensor* t : spans) {
+    if (!lane_span_ok(t, 2)) return fail(LQ_ERR_UNSUPPORTED, "tensor spans exceed 32-bit offsets");
+  }
+  if (!lane_span_ok(A, 1) || !lane_span_ok(D, 1) || !lane_span_ok(dt_bias, 1)) {
+    return fail(LQ_ERR_UNSUPPORTED, "tensor spans exceed 32-bit offsets");
+  }
+  dim3 grid;
+  if ((rc = grid_for(Bn, H, P, p.vbpr_log2, grid)) != LQ_OK) return rc;
+  const bool bcvec = bc_vector_ok(B) && bc_vector_ok(C);
   hipStream_t s = (hipStream_t)stream;
   if (format_bits == 8) {
-    dispatch_update<8>(p, round_mode, vec, grid, s);
+    dispatch_update<8>(p, round_mode, vec, bcvec, grid, s);
   } else {
-    dispatch_update<4>(p, round_mode, vec, grid, s);
+    dispatch_update<4>(p, round_mode, vec, bcvec, grid, s);
   }
   return check_launch("lq_mx_state_update");
 }
@@ -626,10 +732,15 @@ extern "C" int lq_mx_encode(const lq_tensor* state, const lq_tensor* q_state,
   p.P = (int)P;
   p.N = (int)N;
   p.bpr = (int)(N / 16);
+  p.vbpr_log2 = log2_ceil(p.bpr);
   p.key = seed_key(seed);
   p.rng_offset = rng_offset;
-  const int64_t lanes = Bn * H * P * p.bpr;
-  const dim3 grid((unsigned)((lanes + 255) / 256));
+  const lq_tensor* spans[] = {q_state, shared_exp, micro_exp, state, uniform};
+  for (const lq_tensor* t : spans) {
+    if (!lane_span_ok(t, 2)) return fail(LQ_ERR_UNSUPPORTED, "tensor spans exceed 32-bit offsets");
+  }
+  dim3 grid;
+  if ((rc = grid_for(Bn, H, P, p.vbpr_log2, grid)) != LQ_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   if (format_bits == 8) {
     dispatch_encode<8>(p, round_mode, vec, grid, s);
@@ -662,8 +773,13 @@ extern "C" int lq_mx_decode(const lq_tensor* q_state, const lq_tensor* shared_ex
   p.P = (int)P;
   p.N = (int)N;
   p.bpr = (int)(N / 16);
-  const int64_t lanes = Bn * H * P * p.bpr;
-  const dim3 grid((unsigned)((lanes + 255) / 256));
+  p.vbpr_log2 = log2_ceil(p.bpr);
+  const lq_tensor* spans[] = {q_state, shared_exp, micro_exp, out};
+  for (const lq_tensor* t : spans) {
+    if (!lane_span_ok(t, 2)) return fail(LQ_ERR_UNSUPPORTED, "tensor spans exceed 32-bit offsets");
+  }
+  dim3 grid;
+  if ((rc = grid_for(Bn, H, P, p.vbpr_log2, grid)) != LQ_OK) return rc;
   if (vec) {
     hipLaunchKernelGGL(mx_decode_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, p);
   } else {

@@ -22,7 +22,7 @@ def _state(shape, seed, dtype=torch.float32):
     flat[0, :16] = 0.0                                                 # an all-zero block
     flat[1, :16] = 0.0
     flat[1, 3] = 126 * 2.0 ** -7                                       # amax/126 a power of two
-    flat[2, 5] = np.float32(np.ldexp(1 + 2.0 ** -23, -3) * 126)        # inside the log2 band
+    flat[2, 5] = float(np.float32(np.ldexp(1 + 2.0 ** -23, -3) * 126))  # inside the log2 band
     flat[3, :16] *= 1e-20                                              # tiny block
     return h.to(dtype)
 
@@ -67,6 +67,23 @@ def test_encode_decode_state_widths(gpu, n):
     deq = torch.empty(shape, device=gpu)
     _abi.mx_decode(*out, deq)
     assert np.array_equal(deq.cpu().numpy(), omx.mx_decode(*ref))
+
+
+def _assert_state_close(got, ref, rtol=2e-3):
+    """Writeback of an h' computed in another float order: normwise within rtol of the oracle's
+    dequantized state, >= 99.9% of mantissas bit-identical, and every differing value at most one
+    quantization step (of the larger pair scale) away -- a value on a rounding boundary may land
+    on the neighbouring level."""
+    g = omx.mx_decode(*got).astype(np.float64)
+    w = omx.mx_decode(*ref).astype(np.float64)
+    fro = np.linalg.norm(g - w) / np.linalg.norm(w)
+    assert fro <= rtol, f"dequantized state: relative Frobenius error {fro:.3g}"
+    same = np.mean(got[0] == ref[0])
+    assert same > 0.999, f"only {same:.5f} of mantissas bit-identical"
+    step = lambda e, m: omx.exp2_scale(np.repeat(e.astype(np.uint32), 16, -1)
+                                       + np.repeat(m.astype(np.uint32), 2, -1)).astype(np.float64)
+    bound = np.maximum(step(got[1], got[2]), step(ref[1], ref[2]))
+    assert np.all(np.abs(g - w) <= bound * (1 + 1e-6)), "a value moved by more than one level"
 
 
 def _inputs(bsz, nh, p_, n, ng, seed, device, dt_zero=False):
@@ -131,11 +148,7 @@ def test_update_parity(gpu, fb, softplus):
                                         dt_softplus=softplus, format_bits=fb, round_mode=2,
                                         uniform=uni)
     assert_close_rel(out.cpu(), ry, what="y")
-    got = omx.mx_decode(*(a.cpu().numpy() for a in st))
-    want = omx.mx_decode(rq, re_, rm)
-    assert_close_rel(torch.from_numpy(got), torch.from_numpy(want), what="dequantized state")
-    same = np.mean(st[0].cpu().numpy() == rq)
-    assert same > 0.999, f"only {same:.5f} of mantissas bit-identical"
+    _assert_state_close([a.cpu().numpy() for a in st], (rq, re_, rm))
 
 
 def test_update_general_A_and_strides(gpu):
