@@ -10,15 +10,17 @@
 //
 // Columns. The 16 columns are (group m, head h) pairs, j = m*NREP + h, NREP*(128/g) <= 16.
 //
-// QK^T. A = 16 keys x 32 dims of one 32-dim chunk, B = the query dims of that chunk, placed only
-// in the columns whose group m owns the chunk (zero elsewhere). Accumulating the 4 chunks gives,
-// in column (m, h), the group-m partial dot product of head h; scaling by the key scale of group
-// m and summing the columns of equal h (DPP row rotations) gives the score in every column of h.
+// QK^T. Lane (q, r) loads the 16-byte unit q (dims 32q .. 32q+31) of key row r with one dwordx4
+// and feeds dword c of it to MFMA c (A = 16 keys x 32 K slots). B = the matching query dims,
+// placed only in the columns whose group m owns them (zero elsewhere), so after the 4 MFMAs
+// column (m, h) holds the group-m partial dot product of head h; scaling by the key scale of
+// group m and summing the columns of equal h (DPP row rotations) gives the score of head h.
 // Nibbles decode in registers to bf16 with a magic number: bits 0x4300 | (n ^ 8) are the value
 // 136 + n, so the accumulator starts at -136 * sum(q) of the column's dims.
 //
 // P V. A = V^T: 16 dims x 32 keys, B = P' with P'[key][(m, h)] = p[key][h] * vscale[key][m].
-// Lane (q, c) loads dword c of 8 key rows, so MFMA k (k = 0..7) covers dims 8c + k; the output
+// Lane (q, c) loads dword c of key rows q + 4e (e = 0..7; one load instruction reads 4 whole
+// consecutive rows), so MFMA k (k = 0..7) covers dims 8c + k; the output
 // column (m, h) is kept only for dims of group m. P' is split into bf16 hi + lo (two MFMAs, about
 // 16 significant bits). The value offset 136 of the V decode is removed at the end with
 // sum_keys P' from one more MFMA against a ones operand.
@@ -36,8 +38,11 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int FAST_D = 128;
-constexpr int TILE = 32;
+constexpr int SUB = 32;              // keys per MFMA sub-tile (the K depth of the P V product)
+constexpr int NSUB = 1;              // sub-tiles per iteration; one softmax max per iteration
+constexpr int TILE = SUB * NSUB;     // keys per wave iteration
 constexpr int WAVES = 4;
+constexpr float LAZY_LOG2 = 8.0f;    // running-max slack of the lazy softmax rescale
 constexpr uint32_t NIB2 = 0x000F000Fu;
 constexpr int BUF_DWORD3 = 0x00020000;  // raw 32-bit buffer, gfx9 family
 
@@ -80,41 +85,57 @@ __device__ __forceinline__ float column_sum(float x) {
   return x;
 }
 
+template <int G>
 struct TileRegs {
-  uint32_t kw[2][4];  // [16-key half][32-dim chunk]: dword (4*chunk + l/16) of key row l%16
-  uint32_t vw[8];     // dword l%16 of the 8 key rows of this lane's K slots
-  float ksr[2];       // key / value scale words, staged through LDS
-  float vsr[2];
+  static constexpr int SCW = (G * TILE + 63) / 64;  // scale words per lane
+  u32x4_t kq[NSUB][2];      // [sub][16-key half]: 16-byte unit l/16 (dims 32*(l/16) ..) of row l%16
+  uint32_t vw[NSUB][8];     // [sub]: dword l%16 of the 8 key rows of this lane's K slots
+  float ksr[SCW];           // key / value scale words, staged through LDS
+  float vsr[SCW];
 };
 
+// Per-wave bases of this (batch, KV head) block; rows are contiguous (64 packed bytes, G scale
+// words). Each tile builds buffer descriptors whose base is the tile's first key and whose size
+// ends at key S, so the hardware range check (vector + immediate offset; the scalar offset is
+// kept 0 because it is not range-checked) returns 0 for keys past S.
 struct Rsrc {
-  __amdgpu_buffer_rsrc_t k, v, ks, vs;
-  int kvo, vvo, ksvo[2], vsvo[2];  // per-lane byte offsets
-  int krow, vrow, ksrow, vsrow;  // byte strides of one key row
+  const uint8_t* kb;
+  const uint8_t* vb;
+  const float* ksb;
+  const float* vsb;
+  int kvo, vvo;  // per-lane byte offsets inside a tile
 };
 
 template <int G>
-__device__ __forceinline__ void load_tile(const Rsrc& R, int tb, TileRegs& r) {
+__device__ __forceinline__ void load_tile(const Rsrc& R, int tb, int S, TileRegs<G>& r) {
+  tb = __builtin_amdgcn_readfirstlane(tb);  // uniform by construction; lets the descriptors live in SGPRs
+  const int rem = S - tb;  // > 0
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(R.kb + (int64_t)tb * 64), 0, rem * 64, BUF_DWORD3);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(R.vb + (int64_t)tb * 64), 0, rem * 64, BUF_DWORD3);
+  const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(R.ksb + (int64_t)tb * G), 0, rem * G * 4, BUF_DWORD3);
+  const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(R.vsb + (int64_t)tb * G), 0, rem * G * 4, BUF_DWORD3);
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int so = (tb + 16 * t) * R.krow;
+  for (int i = 0; i < TileRegs<G>::SCW; ++i) {
+    const int off = (lane + 64 * i) * 4;  // word (key, group) = key * G + group
+    r.ksr[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, off, 0, 0));
+    r.vsr[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, off, 0, 0));
+  }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      r.kw[t][c] = __builtin_amdgcn_raw_buffer_load_b32(R.k, R.kvo + 16 * c, so, 0);
+  for (int sb = 0; sb < NSUB; ++sb) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      r.kq[sb][t] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, R.kvo + (SUB * sb + 16 * t) * 64, 0, 0));
+
     }
-  }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int so = (tb + 16 * (e >> 2) + (e & 3)) * R.vrow;
-    r.vw[e] = __builtin_amdgcn_raw_buffer_load_b32(R.v, R.vvo, so, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    if (i * 64 < G * TILE) {
-      r.ksr[i] = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(R.ks, R.ksvo[i], tb * R.ksrow, 0));
-      r.vsr[i] = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(R.vs, R.vsvo[i], tb * R.vsrow, 0));
+    for (int e = 0; e < 8; ++e) {
+      r.vw[sb][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, R.vvo + (SUB * sb + 4 * e) * 64, 0, 0);
     }
   }
 }
@@ -124,7 +145,7 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
   constexpr int NCOL = NREP * G;
   constexpr int CPG = 4 / G;  // 32-dim chunks per group
   static_assert(NCOL <= 16, "columns exceed the MFMA tile");
-  __shared__ float sc_lds[WAVES][2][G][TILE];
+  __shared__ float sc_lds[WAVES][2][2][G][TILE];  // [wave][buffer][k/v][group][key]
   __shared__ float o_lds[WAVES][NREP][FAST_D];
   __shared__ float ml_lds[WAVES][2][NREP];
 
@@ -148,21 +169,23 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
   const int colh = c16 % NREP;
   const int colm = colvalid ? c16 / NREP : 0;
 
-  // query operands of the 4 chunks and the column sums for the decode offset
+  // Query operands. Lane (q, .) feeds MFMA c with dword c of its key unit q, i.e. dims
+  // 32q + 8c .. 32q + 8c + 7 (slot order kPerm); the query is placed only in the columns whose
+  // group owns those dims, so each column accumulates exactly its group's partial dot product.
   const uint16_t* qbits = (const uint16_t*)p.q.data;
   const int64_t qbase = b * p.q.s[0] + (int64_t)(kvh * NREP + colh) * p.q.s[1];
   constexpr int kPerm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+  const bool use = colvalid && (q4 / CPG == colm);
   u32x4_t qop[4];
   float qsum = 0.0f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const bool use = colvalid && (c / CPG == colm);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       uint32_t lo = 0, hi = 0;
       if (use) {
-        lo = qbits[qbase + (32 * c + 8 * q4 + kPerm[2 * u]) * p.q.s[2]];
-        hi = qbits[qbase + (32 * c + 8 * q4 + kPerm[2 * u + 1]) * p.q.s[2]];
+        lo = qbits[qbase + (32 * q4 + 8 * c + kPerm[2 * u]) * p.q.s[2]];
+        hi = qbits[qbase + (32 * q4 + 8 * c + kPerm[2 * u + 1]) * p.q.s[2]];
       }
       qsum += bf16_bits_to_float(lo) + bf16_bits_to_float(hi);
       qop[c][u] = lo | (hi << 16);
@@ -172,34 +195,16 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
   qsum += __shfl_xor(qsum, 32, 64);
   const float cinit = -136.0f * qsum;
 
-  // buffer resources over this (batch, KV head); loads past the last key return 0
   Rsrc R;
-  {
-    const uint8_t* kb = p.kp + b * p.kps[0] + kvh * p.kps[1];
-    const uint8_t* vb = p.vp + b * p.vps[0] + kvh * p.vps[1];
-    const float* ksb = p.ks + b * p.kss[0] + kvh * p.kss[1];
-    const float* vsb = p.vs + b * p.vss[0] + kvh * p.vss[1];
-    R.krow = (int)p.kps[2];
-    R.vrow = (int)p.vps[2];
-    R.ksrow = (int)p.kss[2] * 4;
-    R.vsrow = (int)p.vss[2] * 4;
-    R.k = __builtin_amdgcn_make_buffer_rsrc((void*)kb, 0, (S - 1) * R.krow + 64, BUF_DWORD3);
-    R.v = __builtin_amdgcn_make_buffer_rsrc((void*)vb, 0, (S - 1) * R.vrow + 64, BUF_DWORD3);
-    R.ks = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)ksb, 0, ((S - 1) * (int)p.kss[2] + (G - 1) * (int)p.kss[3] + 1) * 4, BUF_DWORD3);
-    R.vs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)vsb, 0, ((S - 1) * (int)p.vss[2] + (G - 1) * (int)p.vss[3] + 1) * 4, BUF_DWORD3);
-    R.kvo = c16 * R.krow + 4 * q4;
-    R.vvo = 4 * q4 * R.vrow + 4 * c16;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int idx = lane + 64 * i;
-      const int tok = idx / G;
-      const int m = idx - tok * G;
-      R.ksvo[i] = (tok * (int)p.kss[2] + m * (int)p.kss[3]) * 4;
-      R.vsvo[i] = (tok * (int)p.vss[2] + m * (int)p.vss[3]) * 4;
-    }
-  }
+  R.kb = p.kp + b * p.kps[0] + kvh * p.kps[1];
+  R.vb = p.vp + b * p.vps[0] + kvh * p.vps[1];
+  R.ksb = p.ks + b * p.kss[0] + kvh * p.kss[1];
+  R.vsb = p.vs + b * p.vss[0] + kvh * p.vss[1];
+  // QK A-row i of a 16-key half is key 4 (i & 3) + (i >> 2), so that output row 4q + r (held by
+  // lane group q) is key 4r + q, and lane group q's 8 keys of a 32-key sub-tile are q + 4e
+  // (e = 4t + r): the V loads of key slot e then cover keys 4e .. 4e+3 contiguously.
+  R.kvo = (4 * (c16 & 3) + (c16 >> 2)) * 64 + 16 * q4;
+  R.vvo = q4 * 64 + 4 * c16;
 
   float m_run = -INFINITY;
   float l_run = 0.0f;
@@ -209,120 +214,171 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
   f32x4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
   const u32x4_t ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
 
-  auto process = [&](const int tb, const TileRegs& cur) {
-    // stage this tile's scales transposed, sc_lds[.][m][key]; fold log2(e)/sqrt(D) into K's
+  // Scales of a tile go to LDS, transposed to [group][key] with log2(e)/sqrt(D) folded into the
+  // key scales, one tile before their use; buffer (tile index & 1).
+  auto stage_scales = [&](const TileRegs<G>& r, const int buf) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < TileRegs<G>::SCW; ++i) {
       const int idx = lane + 64 * i;
       if (idx < G * TILE) {
         const int tok = idx / G;
         const int m = idx - tok * G;
-        sc_lds[wave][0][m][tok] = cur.ksr[i] * p.scale_sm;
-        sc_lds[wave][1][m][tok] = cur.vsr[i];
+        // key 16t + 4r + q is read by lane group q as element r: store it at 16t + 4q + r
+        const int pos = (tok & ~15) | ((tok & 3) << 2) | ((tok >> 2) & 3);
+        sc_lds[wave][buf][0][m][pos] = r.ksr[i] * p.scale_sm;
+        sc_lds[wave][buf][1][m][pos] = r.vsr[i];
       }
     }
+  };
 
-    // scores: 2 halves of 16 keys, 4 chunks each
-    f32x4_t sacc[2];
+  auto process = [&](const int tb, const TileRegs<G>& cur, const TileRegs<G>& next,
+                     const bool has_next) {
+    const int buf = ((tb - w0) / TILE) & 1;
+    if (has_next) stage_scales(next, buf ^ 1);
+    // scores: per sub-tile 2 halves of 16 keys, 4 chunks each
+    f32x4_t sacc[NSUB][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      sacc[t] = f32x4_t{cinit, cinit, cinit, cinit};
+    for (int sb = 0; sb < NSUB; ++sb) {
+      sacc[sb][0] = f32x4_t{cinit, cinit, cinit, cinit};
+      sacc[sb][1] = sacc[sb][0];
+      // the two 16-key halves are independent chains: interleave them
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        sacc[t] = mfma_bf16(decode_k(cur.kw[t][c]), qop[c], sacc[t]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          sacc[sb][t] = mfma_bf16(decode_k(cur.kq[sb][t][c]), qop[c], sacc[sb][t]);
+        }
       }
     }
     __builtin_amdgcn_wave_barrier();
-    const f32x4_t ks0 = *(const f32x4_t*)&sc_lds[wave][0][colm][4 * q4];
-    const f32x4_t ks1 = *(const f32x4_t*)&sc_lds[wave][0][colm][16 + 4 * q4];
-    const f32x4_t vs0 = *(const f32x4_t*)&sc_lds[wave][1][colm][4 * q4];
-    const f32x4_t vs1 = *(const f32x4_t*)&sc_lds[wave][1][colm][16 + 4 * q4];
 
-    float s[8];
+    // key slot e of sub-tile sb (e = 4t + r) is key tb + 32 sb + 16 t + 4 r + (l/16)
+    float s[NSUB][8];
+    f32x4_t vsc[NSUB][2];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      s[r] = column_sum<NREP>(sacc[0][r] * ks0[r]);
-      s[4 + r] = column_sum<NREP>(sacc[1][r] * ks1[r]);
+    for (int sb = 0; sb < NSUB; ++sb) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const f32x4_t ks4 = *(const f32x4_t*)&sc_lds[wave][buf][0][colm][SUB * sb + 16 * t + 4 * q4];
+        vsc[sb][t] = *(const f32x4_t*)&sc_lds[wave][buf][1][colm][SUB * sb + 16 * t + 4 * q4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[sb][4 * t + r] = column_sum<NREP>(sacc[sb][t][r] * ks4[r]);
+      }
     }
     if (p.mask != nullptr) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int tok = tb + 16 * (e >> 2) + 4 * q4 + (e & 3);
-        s[e] += (tok < p.mask_len) ? p.mask[b * p.mask_sb + (int64_t)tok * p.mask_sk] : -INFINITY;
+      for (int sb = 0; sb < NSUB; ++sb) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int tok = tb + SUB * sb + 16 * (e >> 2) + 4 * (e & 3) + q4;
+          s[sb][e] += (tok < p.mask_len) ? p.mask[b * p.mask_sb + (int64_t)tok * p.mask_sk]
+                                         : -INFINITY;
+        }
       }
     }
     if (tb + TILE > w1) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int tok = tb + 16 * (e >> 2) + 4 * q4 + (e & 3);
-        s[e] = tok < w1 ? s[e] : -INFINITY;
+      for (int sb = 0; sb < NSUB; ++sb) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int tok = tb + SUB * sb + 16 * (e >> 2) + 4 * (e & 3) + q4;
+          s[sb][e] = tok < w1 ? s[sb][e] : -INFINITY;
+        }
       }
     }
-    float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
-                     fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m_run, mt);
-    // acc and l are still zero while m_run is -inf: no rescale needed then
-    const float alpha = (m_run == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-    float pe[8];
+    // Lazy rescaling: p = 2^(s - m_run) with a running max that only moves when a score exceeds
+    // it by more than LAZY_LOG2 (p <= 2^LAZY_LOG2 otherwise), so the cross-lane max and the
+    // accumulator rescale leave the common path. The first tile always takes the update.
+    float lm = -INFINITY;
+#pragma unroll
+    for (int sb = 0; sb < NSUB; ++sb) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lm = fmaxf(lm, s[sb][e]);
+    }
+    if (__any(lm > m_run + LAZY_LOG2)) {
+      float mt = fmaxf(lm, __shfl_xor(lm, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float m_new = fmaxf(m_run, mt);
+      // acc and l are still zero while m_run is -inf: no rescale needed then
+      const float alpha = (m_run == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      if (alpha != 1.0f) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] *= alpha;
+        corr *= alpha;
+        l_run *= alpha;
+      }
+      m_run = m_new;
+    }
     float psum = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      pe[e] = (s[e] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[e] - m_new);
-      psum += pe[e];
-    }
-    l_run = l_run * alpha + psum;
-    if (__any(alpha != 1.0f)) {
+    for (int sb = 0; sb < NSUB; ++sb) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) acc[k] *= alpha;
-      corr *= alpha;
+      for (int e = 0; e < 8; ++e) {
+        s[sb][e] = (s[sb][e] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[sb][e] - m_run);
+        psum += s[sb][e];
+      }
     }
-    m_run = m_new;
+    l_run += psum;
 
-    // P' = p * vscale, split into bf16 hi + lo
-    u32x4_t bhi, blo;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int e = 2 * u;
-      const float a0 = pe[e] * (e < 4 ? vs0[e] : vs1[e - 4]);
-      const float a1 = pe[e + 1] * (e + 1 < 4 ? vs0[e + 1] : vs1[e - 3]);
-      const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a0, a1}, bf16x2_t));
-      const float r0 = a0 - __builtin_bit_cast(float, h << 16);
-      const float r1 = a1 - __builtin_bit_cast(float, h & 0xffff0000u);
-      bhi[u] = h;
-      blo[u] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t));
+    for (int sb = 0; sb < NSUB; ++sb) {
+      // P' = p * vscale, split into bf16 hi + lo
+      u32x4_t bhi, blo;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = 2 * u;
+        const float a0 = s[sb][e] * vsc[sb][e >> 2][e & 3];
+        const float a1 = s[sb][e + 1] * vsc[sb][(e + 1) >> 2][(e + 1) & 3];
+        const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a0, a1}, bf16x2_t));
+        const float r0 = a0 - __builtin_bit_cast(float, h << 16);
+        const float r1 = a1 - __builtin_bit_cast(float, h & 0xffff0000u);
+        bhi[u] = h;
+        blo[u] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t));
+      }
+      // V decode: pair the key slots (2u, 2u+1), nibble k of each dword -> MFMA k
+      uint32_t ylo[4], yhi[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        ylo[u] = __builtin_amdgcn_perm(cur.vw[sb][2 * u + 1], cur.vw[sb][2 * u], 0x05040100u);
+        yhi[u] = __builtin_amdgcn_perm(cur.vw[sb][2 * u + 1], cur.vw[sb][2 * u], 0x07060302u);
+      }
+      // four dims-sets at a time: their hi products, then their lo products, so that the two
+      // MFMAs into one accumulator are separated by three independent ones
+#pragma unroll
+      for (int k0 = 0; k0 < 8; k0 += 4) {
+        u32x4_t a[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) a[j][u] = nib_pair((k0 < 4 ? ylo[u] : yhi[u]) >> (4 * j));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[k0 + j] = mfma_bf16(a[j], bhi, acc[k0 + j]);
+        if (k0 == 0) corr = mfma_bf16(ones, bhi, corr);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[k0 + j] = mfma_bf16(a[j], blo, acc[k0 + j]);
+        if (k0 == 4) corr = mfma_bf16(ones, blo, corr);
+      }
     }
-
-    // V decode: pair the key slots (2u, 2u+1), nibble k of each dword -> MFMA k
-    uint32_t ylo[4], yhi[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      ylo[u] = __builtin_amdgcn_perm(cur.vw[2 * u + 1], cur.vw[2 * u], 0x05040100u);
-      yhi[u] = __builtin_amdgcn_perm(cur.vw[2 * u + 1], cur.vw[2 * u], 0x07060302u);
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      u32x4_t a;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) a[u] = nib_pair((k < 4 ? ylo[u] : yhi[u]) >> (4 * (k & 3)));
-      acc[k] = mfma_bf16(a, bhi, acc[k]);
-      acc[k] = mfma_bf16(a, blo, acc[k]);
-    }
-    corr = mfma_bf16(ones, bhi, corr);
-    corr = mfma_bf16(ones, blo, corr);
     __builtin_amdgcn_wave_barrier();
   };
 
-  // two register stages, ping-pong: the next tile's loads are in flight during this tile's math
-  TileRegs ra, rb;
-  if (w0 < w1) load_tile<G>(R, w0, ra);
-  for (int tb = w0; tb < w1; tb += 2 * TILE) {
-    if (tb + TILE < w1) load_tile<G>(R, tb + TILE, rb);
-    process(tb, ra);
+  // three register stages: two tiles of loads stay in flight while a third is processed
+  TileRegs<G> ra, rb, rc;
+  if (w0 < w1) {
+    load_tile<G>(R, w0, S, ra);
+    stage_scales(ra, 0);
+  }
+  if (w0 + TILE < w1) load_tile<G>(R, w0 + TILE, S, rb);
+  for (int tb = w0; tb < w1; tb += 3 * TILE) {
+    if (tb + 2 * TILE < w1) load_tile<G>(R, tb + 2 * TILE, S, rc);
+    process(tb, ra, rb, tb + TILE < w1);
     if (tb + TILE >= w1) break;
-    if (tb + 2 * TILE < w1) load_tile<G>(R, tb + 2 * TILE, ra);
-    process(tb + TILE, rb);
+    if (tb + 3 * TILE < w1) load_tile<G>(R, tb + 3 * TILE, S, ra);
+    process(tb + TILE, rb, rc, tb + 2 * TILE < w1);
+    if (tb + 2 * TILE >= w1) break;
+    if (tb + 4 * TILE < w1) load_tile<G>(R, tb + 4 * TILE, S, rb);
+    process(tb + 2 * TILE, rc, ra, tb + 3 * TILE < w1);
   }
 
   // per-wave partial -> LDS
@@ -397,22 +453,18 @@ bool fast_path_ok(const AttnParams& p) {
   if (force_generic()) return false;
   if (!fast_path_shape_ok(p.D, p.g, p.Hq, p.Hkv)) return false;
   if (p.q.dtype != LQ_BF16) return false;
-  if (p.kps[3] != 1 || p.vps[3] != 1) return false;
-  const int64_t strides[6] = {p.kps[0], p.kps[1], p.kps[2], p.vps[0], p.vps[1], p.vps[2]};
+  // contiguous key rows: 64 packed bytes per key, D/g scale words per key
+  const int64_t G = FAST_D / p.g;
+  if (p.kps[3] != 1 || p.vps[3] != 1 || p.kps[2] != 64 || p.vps[2] != 64) return false;
+  if (p.kss[3] != 1 || p.vss[3] != 1 || p.kss[2] != G || p.vss[2] != G) return false;
+  const int64_t strides[4] = {p.kps[0], p.kps[1], p.vps[0], p.vps[1]};
   for (int64_t s : strides) {
     if (s % 4 != 0) return false;
   }
   if (((uintptr_t)p.kp & 3) != 0 || ((uintptr_t)p.vp & 3) != 0) return false;
-  // byte offsets inside one (batch, KV head) block are 32-bit buffer offsets
-  const int64_t lim = (int64_t)1 << 31;
-  if (p.S * std::max(p.kps[2], p.vps[2]) >= lim) return false;
-  if ((p.S * std::max(p.kss[2], p.vss[2]) + 4 * std::max(p.kss[3], p.vss[3])) * 4 >= lim) {
-    return false;
-  }
-  if (p.kss[2] < 0 || p.kss[3] < 0 || p.vss[2] < 0 || p.vss[3] < 0 || p.kps[2] <= 0 ||
-      p.vps[2] <= 0) {
-    return false;
-  }
+  if (((uintptr_t)p.ks & 3) != 0 || ((uintptr_t)p.vs & 3) != 0) return false;
+  // buffer sizes of one (batch, KV head) block are 32-bit
+  if (p.S * 64 >= ((int64_t)1 << 31)) return false;
   return true;
 }
 
