@@ -8,6 +8,7 @@ the library must be built (python -m layer_quant_amd.build) and tensors must liv
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
@@ -97,16 +98,18 @@ def _declare(lib: ctypes.CDLL) -> None:
 
 
 def lib() -> ctypes.CDLL:
-    """Load liblayer_quant.so once; raise if it has not been built."""
+    """Load liblayer_quant.so once (the in-tree build, or the file LQ_LIBRARY names); raise if
+    it has not been built."""
     global _lib
     if _lib is None:
         with _lib_lock:
             if _lib is None:
-                if not LIB_PATH.exists():
+                path = Path(os.environ.get("LQ_LIBRARY") or LIB_PATH)
+                if not path.exists():
                     raise RuntimeError(
-                        f"{LIB_PATH} is not built; run `python -m layer_quant_amd.build` "
+                        f"{path} is not built; run `python -m layer_quant_amd.build` "
                         "(or __graft_entry__.build()) first")
-                handle = ctypes.CDLL(str(LIB_PATH))
+                handle = ctypes.CDLL(str(path))
                 _declare(handle)
                 _lib = handle
     return _lib

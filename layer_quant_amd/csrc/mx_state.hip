@@ -15,13 +15,16 @@
 // the MX4 path does not round-trip an fp32 state through HBM as the reference does.
 //
 // Encode of a block (bit-exact with the torch formula):
-//   t = max(absmax / (2M), 1e-30)           IEEE fp32 division
+//   t = max(absmax / (2M), 1e-30)           correctly rounded fp32 quotient (two fmas)
 //   e = clamp(ceil(log2 t) + 127, 1, 254)    ceil of the correctly rounded fp32 log2, computed
 //                                            exactly from t's exponent and mantissa bits
 //   base = absmax == 0 ? 1 : 2^(e-127);  micro = pair_absmax > M*base
 //   qa = min(|v| / (base*2^micro), M)        as a product with the exact reciprocal
 //   level = rint(qa) | floor(qa + 0.5) | floor(qa) + (u < qa - floor(qa))   (always <= M)
+// The counter mode (LQ_ROUND_SR_COUNTER) draws 16-bit integers u16 and dithers in fixed point:
+//   T = trunc(clamp(v * 2^16 / (base*2^micro), -M*2^16, M*2^16)),  level = (T + u16) >> 16
 #include <math.h>
+#include <stdlib.h>
 
 #include "lq_common.h"
 
@@ -41,6 +44,9 @@ struct MxUpdateParams {
   int has_dtb, has_D, has_z, softplus, a_row_const;
   uint32_t key;
   uint64_t rng_offset;
+  // rows kernel, counter mode: hash of the pair counters' common high word, and the low word of
+  // rng_offset / 2 (the launch's pair counters share one high word)
+  uint32_t kh, lo_base;
 };
 
 struct MxCodecParams {
@@ -122,10 +128,10 @@ __device__ __forceinline__ int ceil_log2_exact(float t) {
   return mant == 0 ? E : (mant <= thr ? E : E + 1);
 }
 
-// Counter-based 16-bit uniforms of one 16-value block, returned as u * 2^16 (exact integers):
-// element n draws counter c = rng_offset + row*N + n; pair c>>1 hashes to 32 bits, the even
-// element takes the low half.
-__device__ __forceinline__ void block_uniforms(uint32_t key, uint64_t c0, float (&u16)[16]) {
+// Counter-based draws of one 16-value block: element n draws counter c = rng_offset + row*N + n;
+// pair c>>1 hashes to the 32-bit word pw[k] (k = pair within the block), whose low half is the
+// even element's 16-bit draw and whose high half is the odd element's.
+__device__ __forceinline__ void block_words(uint32_t key, uint64_t c0, uint32_t (&pw)[8]) {
   const uint64_t pc0 = c0 >> 1;
   const uint32_t lo0 = (uint32_t)pc0;
   const uint32_t hi0 = (uint32_t)(pc0 >> 32);
@@ -140,16 +146,42 @@ __device__ __forceinline__ void block_uniforms(uint32_t key, uint64_t c0, float 
     for (int k = 0; k < 8; ++k) kh[k] = kh0;
   }
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const uint32_t bits = lowbias32((lo0 + (uint32_t)k) ^ kh[k]);
-    u16[2 * k] = (float)(bits & 0xffffu);
-    u16[2 * k + 1] = (float)(bits >> 16);
-  }
+  for (int k = 0; k < 8; ++k) pw[k] = lowbias32((lo0 + (uint32_t)k) ^ kh[k]);
 }
 
-// Encode 16 values. `u16` holds the stochastic-rounding uniforms scaled by 2^16 (so that the
-// comparison u < frac becomes u16 < frac * 2^16, both sides exact), unused otherwise.
-// The reference's final min(level, M) is omitted: every mode already yields level <= M.
+// Shared exponent of a block from its absmax: eb = clamp(ceil(log2 t) + 127, 1, 254) with
+// t = max(RN(absmax / 2M), 1e-30), and ebase = 127 for an all-zero block. RN(a / 2M) is
+// q + (a - 2M q) / 2M evaluated as q = RN(a c), r = fma(-q, 2M, a) (exact), RN(fma(r, c, q)) with
+// c = RN(1 / 2M); that equals the IEEE quotient for every positive fp32 a once the 1e-30 floor
+// is applied (checked exhaustively for 2M = 14 and 126; +inf is passed through).
+// ceil(log2 t) is E + 1 unless t lies within T(E) <= 44 ulps above 2^E (T = 0 for E = 0), where
+// the exact rule decides. Returns whether it did: only then (t within the band, or +inf) can
+// 2^e fall below absmax / 2M, so that |v| / (base * 2^micro) may exceed M. Elsewhere e = E + 1
+// and absmax / 2M <= t (1 + 2^-24) < 2^(E+1) (the eb clamp only raises the scale), so every
+// pair's qa <= M exactly.
+template <int FB>
+__device__ __forceinline__ bool block_exponent(float amax, int& eb, int& ebase) {
+#pragma clang fp contract(off)
+  constexpr float TWO_M = FB == 8 ? 126.0f : 14.0f;
+  constexpr float C = 1.0f / TWO_M;
+  const float q = amax * C;
+  const float r = __builtin_fmaf(-q, TWO_M, amax);
+  float t = __builtin_fmaf(r, C, q);
+  t = (amax == INFINITY) ? amax : t;
+  t = fmaxf(t, 1.0e-30f);
+  const uint32_t bits = __float_as_uint(t);
+  int e = (int)(bits >> 23) - 126;
+  const bool band = (bits & 0x7fffffu) <= 44u;
+  if (band) e = ceil_log2_exact(t);
+  eb = min(max(e + 127, 1), 254);
+  ebase = (amax == 0.0f) ? 127 : eb;
+  return band;
+}
+
+// Encode 16 values in the nearest-even, half-up or supplied-uniform mode. `u16` holds the
+// supplied uniforms scaled by 2^16 (so that the comparison u < frac becomes u16 < frac * 2^16,
+// both sides exact), unused otherwise. The reference's final min(level, M) is omitted: every mode
+// already yields level <= M.
 template <int FB, int RMODE>
 __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16)[16],
                                          uint32_t (&qw)[4], uint32_t (&mw)[2], uint32_t& eb_out) {
@@ -162,9 +194,8 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16
     pa[k] = fmaxf(fabsf(v[2 * k]), fabsf(v[2 * k + 1]));
     amax = fmaxf(amax, pa[k]);
   }
-  const float t = fmaxf(amax / (2.0f * M), 1.0e-30f);
-  const int eb = min(max(ceil_log2_exact(t) + 127, 1), 254);
-  const int ebase = (amax == 0.0f) ? 127 : eb;
+  int eb, ebase;
+  block_exponent<FB>(amax, eb, ebase);
   const float thr = M * __uint_as_float((uint32_t)ebase << 23);
   // exact reciprocals of the pair scales 2^(se-127), se = ebase + micro: normal for se <= 253,
   // the subnormal 2^-127 for se = 254, and 0 for se = 255 (scale +inf; only reachable when
@@ -202,6 +233,59 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16
   for (int w = 0; w < 4; ++w) {
     const uint32_t lo = __builtin_amdgcn_perm((uint32_t)qi[4 * w + 1], (uint32_t)qi[4 * w], 0x0c0c0400u);
     const uint32_t hi = __builtin_amdgcn_perm((uint32_t)qi[4 * w + 3], (uint32_t)qi[4 * w + 2], 0x04000c0cu);
+    qw[w] = lo | hi;
+  }
+  mw[0] = mb[0] | (mb[1] << 8) | (mb[2] << 16) | (mb[3] << 24);
+  mw[1] = mb[4] | (mb[5] << 8) | (mb[6] << 16) | (mb[7] << 24);
+  eb_out = (uint32_t)eb;
+}
+
+// Encode 16 values in the counter mode: T = v * 2^(143 - se) with se = ebase + micro (one exact
+// fp32 scaling, = v / pair_scale * 2^16), clamped to +-M*2^16, truncated toward zero; the level
+// (T + u16) >> 16 is byte 2 of the 32-bit sum, which the packing picks directly.
+template <int FB>
+__device__ __forceinline__ void encode16_dither(const float (&v)[16], const uint32_t (&pw)[8],
+                                                uint32_t (&qw)[4], uint32_t (&mw)[2],
+                                                uint32_t& eb_out) {
+#pragma clang fp contract(off)
+  constexpr float M = FB == 8 ? 63.0f : 7.0f;
+  constexpr float MT = M * 65536.0f;
+  float pa[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    pa[k] = fmaxf(fabsf(v[2 * k]), fabsf(v[2 * k + 1]));
+    amax = fmaxf(amax, pa[k]);
+  }
+  int eb, ebase;
+  const bool band = block_exponent<FB>(amax, eb, ebase);
+  const float thr = M * __uint_as_float((uint32_t)ebase << 23);
+  const int sh0 = 143 - ebase;
+  const int sh1 = sh0 - 1;
+  float t[16];
+  uint32_t mb[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const bool mi = pa[k] > thr;
+    const int sh = mi ? sh1 : sh0;
+    t[2 * k] = ldexpf(v[2 * k], sh);
+    t[2 * k + 1] = ldexpf(v[2 * k + 1], sh);
+    mb[k] = mi ? 1u : 0u;
+  }
+  if (band) {  // rare: the exponent came from the exact rule (see block_exponent)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] = __builtin_amdgcn_fmed3f(t[i], -MT, MT);
+  }
+  int sum[16];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    sum[2 * k] = (int)t[2 * k] + (int)(pw[k] & 0xffffu);
+    sum[2 * k + 1] = (int)t[2 * k + 1] + (int)(pw[k] >> 16);
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)sum[4 * w + 1], (uint32_t)sum[4 * w], 0x0c0c0602u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)sum[4 * w + 3], (uint32_t)sum[4 * w + 2], 0x06020c0cu);
     qw[w] = lo | hi;
   }
   mw[0] = mb[0] | (mb[1] << 8) | (mb[2] << 16) | (mb[3] << 24);
@@ -291,12 +375,11 @@ __device__ __forceinline__ void load16(const char* base, int dtype, int stride, 
   }
 }
 
+// Supplied uniforms of one block (LQ_ROUND_SR_UNIFORM) scaled by 2^16; zeros otherwise.
 template <int RMODE>
-__device__ __forceinline__ void block_u16(const View& uni, uint32_t key, uint64_t c0, int b, int h,
-                                          int pp, int n0, float (&u16)[16]) {
-  if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
-    block_uniforms(key, c0, u16);
-  } else if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {
+__device__ __forceinline__ void block_u16(const View& uni, int b, int h, int pp, int n0,
+                                          float (&u16)[16]) {
+  if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {
     const float* ub = (const float*)uni.data + ((int64_t)b * uni.s[0] + (int64_t)h * uni.s[1]);
     const int off = pp * (int)uni.s[2] + n0 * (int)uni.s[3];
 #pragma unroll
@@ -306,6 +389,23 @@ __device__ __forceinline__ void block_u16(const View& uni, uint32_t key, uint64_
   } else {
 #pragma unroll
     for (int i = 0; i < 16; ++i) u16[i] = 0.0f;
+  }
+}
+
+// Writeback encode of one block in mode RMODE; c0 = counter of the block's first element.
+template <int FB, int RMODE>
+__device__ __forceinline__ void encode_block(const float (&v)[16], const View& uni, uint32_t key,
+                                             uint64_t c0, int b, int h, int pp, int n0,
+                                             uint32_t (&qw)[4], uint32_t (&mw)[2],
+                                             uint32_t& eb) {
+  if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
+    uint32_t pw[8];
+    block_words(key, c0, pw);
+    encode16_dither<FB>(v, pw, qw, mw, eb);
+  } else {
+    float u16[16];
+    block_u16<RMODE>(uni, b, h, pp, n0, u16);
+    encode16<FB, RMODE>(v, u16, qw, mw, eb);
   }
 }
 
@@ -382,13 +482,143 @@ __global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
   }
 
   // writeback encode (ms.py:168-222, 512-544)
-  float u16[16];
   const uint64_t row = ((uint64_t)b * p.H + h) * p.P + pp;
-  block_u16<RMODE>(p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0, b, h, pp, n0,
-                   u16);
   uint32_t eo_bits;
-  encode16<FB, RMODE>(hv, u16, qw, mw, eo_bits);
+  encode_block<FB, RMODE>(hv, p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0, b,
+                          h, pp, n0, qw, mw, eo_bits);
   if (L.active) store_block<VEC>(qp, mp, ep, qw, mw, eo_bits);
+}
+
+// Row-sum over the 2^BPR_LOG2 adjacent lanes of a state row with DPP moves: quad swaps, then the
+// half-row mirror (lane i <-> 7 - i) and the row mirror (i <-> 15 - i), each pairing every lane
+// with one in the other half of its group.
+template <int BPR_LOG2>
+__device__ __forceinline__ float row_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+  if constexpr (BPR_LOG2 >= 3) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
+  }
+  if constexpr (BPR_LOG2 >= 4) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
+  }
+  return v;
+}
+
+// Row kernel geometry: 256 threads, 2 rows per lane, so 2 * 256 / (N/16) rows per workgroup
+// (64 = one Nemotron-H head at N = 128).
+constexpr int ROWS_PER_LANE = 2;
+template <int BPR_LOG2>
+constexpr int rows_per_group() { return ROWS_PER_LANE * (256 >> BPR_LOG2); }
+
+// Update of the model's decode call (ms.py:97-222, 289-544 for the Nemotron-H layout): state rows
+// contiguous (row stride N), B and C bf16 with a contiguous d_state, and dt, dt_bias, A and D
+// constant within a head (stride 0 along head_dim, A also along d_state), as the model passes
+// them. Grid (ceil(P / rows_per_group), H, B), 256 threads; lane (slot, blk) owns block column
+// blk of rows slot and slot + SLOTS (SLOTS = 256 / (N/16)), so B*dt and C are decoded once for two
+// rows, and every wave load covers 1 KB of consecutive state rows. Same arithmetic as mx_update_kernel in the (B*dt)*x order; in
+// the counter mode rng_offset is a multiple of 16, so a block's pair counters are lo0 | k and
+// lowbias32's first step folds into one per-block word.
+template <int FB, int RMODE, int BPR_LOG2>
+__global__ __launch_bounds__(256) void mx_update_rows_kernel(MxUpdateParams p) {
+  constexpr int BPR = 1 << BPR_LOG2;
+  constexpr int N = 16 * BPR;
+  constexpr int R = ROWS_PER_LANE;
+  constexpr int SLOTS = 256 >> BPR_LOG2;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int blk = threadIdx.x & (BPR - 1);
+  const int slot = threadIdx.x >> BPR_LOG2;
+  const int n0 = blk * 16;
+
+  int8_t* qb = p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1] + n0;
+  uint8_t* mb = p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1] + blk * 8;
+  uint8_t* eb = p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1] + blk;
+  const char* xb = vbase(p.x, b, h);
+  int pp[R];
+  bool act[R];
+  uint32_t qw[R][4], mw[R][2], ev[R];
+  float xv[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    pp[r] = blockIdx.x * rows_per_group<BPR_LOG2>() + r * SLOTS + slot;
+    act[r] = pp[r] < p.P;
+    const int pc = act[r] ? pp[r] : p.P - 1;
+    load_block<true>(qb + pc * N, mb + pc * (N / 2), eb + pc * (N / 16), qw[r], mw[r], ev[r]);
+    xv[r] = ldf(xb, p.x.dtype, __umul24(pc, (uint32_t)p.x.s[2]));
+  }
+
+  // head scalars (ms.py:134-139); exp and log use the hardware transcendentals (relative error
+  // ~1e-6, far inside the 2e-3 output tolerance)
+  float dtv = ldf(vbase(p.dt, b, h), p.dt.dtype, 0);
+  if (p.has_dtb) dtv += ldf(vbase(p.dtb, h, 0), p.dtb.dtype, 0);
+  if (p.softplus) dtv = dtv <= 20.0f ? __logf(1.0f + __expf(dtv)) : dtv;
+  const float dA = __expf(ldf(vbase(p.A, h, 0), p.A.dtype, 0) * dtv);
+  const float Dh = p.has_D ? ldf(vbase(p.D, h, 0), p.D.dtype, 0) : 0.0f;
+  const int grp = h / p.ratio;
+  float Bd[16], Cv[16];
+  load16<true>(vbase(p.B, b, grp), LQ_BF16, 1, n0, Bd);
+  load16<true>(vbase(p.C, b, grp), LQ_BF16, 1, n0, Cv);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) Bd[i] *= dtv;
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    // h' = h * exp(A dt) + (B dt) x, with the decay folded into the pair scale (exact)
+    float hv[16];
+    const uint32_t evs = ev[r] << 23;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t mi = (mw[r][k >> 2] >> (8 * (k & 3))) & 0xffu;
+      const float sdA = __uint_as_float((mi << 23) + evs) * dA;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int n = 2 * k + i;
+        const float qv = (float)(int)(int8_t)(qw[r][n >> 2] >> (8 * (n & 3)));
+        hv[n] = fmaf(qv, sdA, Bd[n] * xv[r]);
+      }
+    }
+    float ypart = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ypart = fmaf(hv[i], Cv[i], ypart);
+    const float y0 = row_sum<BPR_LOG2>(ypart);
+    if (act[r] && blk == 0) {
+      float y = y0;
+      if (p.has_D) y += xv[r] * Dh;
+      if (p.has_z) y *= ldf(vbase(p.z, b, h), p.z.dtype, __umul24(pp[r], (uint32_t)p.z.s[2]));
+      char* ob = (char*)vbase(p.out, b, h);
+      const int oi = __umul24(pp[r], (uint32_t)p.out.s[2]);
+      if (p.out.dtype == LQ_BF16) {
+        ((uint16_t*)ob)[oi] = float_to_bf16_bits(y);
+      } else if (p.out.dtype == LQ_F16) {
+        ((_Float16*)ob)[oi] = (_Float16)y;
+      } else {
+        ((float*)ob)[oi] = y;
+      }
+    }
+
+    // writeback encode (ms.py:168-222, 512-544)
+    uint32_t qo[4], mo[2], eo;
+    if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
+      const uint32_t idx = ((uint32_t)((b * p.H + h) * p.P + pp[r]) * (uint32_t)N + (uint32_t)n0) >> 1;
+      uint32_t base = (p.lo_base + idx) ^ p.kh;
+      base ^= base >> 16;
+      uint32_t pw[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        uint32_t x = base ^ (uint32_t)k;
+        x *= 0x7feb352du;
+        x ^= x >> 15;
+        x *= 0x846ca68bu;
+        pw[k] = x ^ (x >> 16);
+      }
+      encode16_dither<FB>(hv, pw, qo, mo, eo);
+    } else {
+      float u16[16];
+      block_u16<RMODE>(p.uni, b, h, act[r] ? pp[r] : p.P - 1, n0, u16);
+      encode16<FB, RMODE>(hv, u16, qo, mo, eo);
+    }
+    if (act[r]) store_block<true>(qb + pp[r] * N, mb + pp[r] * (N / 2), eb + pp[r] * (N / 16), qo, mo, eo);
+  }
 }
 
 template <int FB, int RMODE, bool VEC>
@@ -402,12 +632,10 @@ __global__ __launch_bounds__(256) void mx_encode_kernel(MxCodecParams p) {
   const int voff = pp * (int)p.v.s[2] + n0 * (int)p.v.s[3];
 #pragma unroll
   for (int i = 0; i < 16; ++i) v[i] = ldf(vb, p.v.dtype, voff + i * (int)p.v.s[3]);
-  float u16[16];
   const uint64_t row = ((uint64_t)b * p.H + h) * p.P + pp;
-  block_u16<RMODE>(p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0, b, h, pp, n0,
-                   u16);
   uint32_t qw[4], mw[2], eb;
-  encode16<FB, RMODE>(v, u16, qw, mw, eb);
+  encode_block<FB, RMODE>(v, p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0, b, h,
+                          pp, n0, qw, mw, eb);
   int8_t* qp = p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1] + pp * (int)p.st.qs[2] + n0;
   uint8_t* mp = p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1] + pp * (int)p.st.ms[2] + L.blk * 8;
   uint8_t* ep = p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1] + pp * (int)p.st.es[2] + L.blk;
@@ -618,6 +846,65 @@ static void dispatch_encode(const MxCodecParams& p, int rmode, bool vec, dim3 gr
   }
 }
 
+template <int FB, int BPR_LOG2>
+static void launch_rows(const MxUpdateParams& p, int rmode, dim3 grid, hipStream_t st) {
+  const dim3 block(256);
+  switch (rmode) {
+    case LQ_ROUND_NEAREST_EVEN:
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_NEAREST_EVEN, BPR_LOG2>), grid,
+                         block, 0, st, p);
+      break;
+    case LQ_ROUND_HALF_UP:
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_HALF_UP, BPR_LOG2>), grid, block, 0,
+                         st, p);
+      break;
+    case LQ_ROUND_SR_UNIFORM:
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_UNIFORM, BPR_LOG2>), grid,
+                         block, 0, st, p);
+      break;
+    default:
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_COUNTER, BPR_LOG2>), grid,
+                         block, 0, st, p);
+      break;
+  }
+}
+
+template <int FB>
+static void dispatch_rows(const MxUpdateParams& p, int rmode, dim3 grid, hipStream_t st) {
+  switch (p.vbpr_log2) {
+    case 2: launch_rows<FB, 2>(p, rmode, grid, st); break;
+    case 3: launch_rows<FB, 3>(p, rmode, grid, st); break;
+    default: launch_rows<FB, 4>(p, rmode, grid, st); break;
+  }
+}
+
+// The rows kernel's preconditions (else the general kernel runs): d_state 64, 128 or 256;
+// vector-aligned state with contiguous rows; bf16 B/C with contiguous d_state; dt, dt_bias, A, D
+// constant within a head; in the counter mode rng_offset a multiple of 16 and all pair counters
+// of the launch sharing one high word, with fewer than 2^32 state elements.
+static bool rows_path_ok(const MxUpdateParams& p, bool vec, bool bcvec, const lq_tensor* dt,
+                         const lq_tensor* dt_bias, const lq_tensor* A, const lq_tensor* D,
+                         int round_mode, int64_t total) {
+  const char* force = getenv("LQ_MX_FORCE_GENERIC");
+  if (force != nullptr && force[0] != '\0' && force[0] != '0') return false;
+  if (!vec || !bcvec) return false;
+  if (p.N != 64 && p.N != 128 && p.N != 256) return false;
+  if (p.st.qs[2] != p.N || p.st.ms[2] != p.N / 2 || p.st.es[2] != p.N / 16) return false;
+  if (dt->stride[2] != 0 || A->stride[1] != 0 || A->stride[2] != 0) return false;
+  // per-row offsets of x, z and out are 24-bit products
+  const int64_t lim = (int64_t)1 << 23;
+  if (p.P * p.x.s[2] >= lim || p.P * p.out.s[2] >= lim || p.P * p.z.s[2] >= lim) return false;
+  if (dt_bias != nullptr && dt_bias->stride[1] != 0) return false;
+  if (D != nullptr && D->stride[1] != 0) return false;
+  if (round_mode == LQ_ROUND_SR_COUNTER) {
+    if (p.rng_offset % 16 != 0 || total >= ((int64_t)1 << 32)) return false;
+    const uint64_t first = p.rng_offset >> 1;
+    const uint64_t last = (p.rng_offset + (uint64_t)total - 1) >> 1;
+    if ((first >> 32) != (last >> 32) || last < first) return false;
+  }
+  return true;
+}
+
 static int grid_for(int64_t Bn, int64_t H, int64_t P, int vbpr_log2, dim3& grid) {
   if (Bn > 65535 || H > 65535) {
     return fail(LQ_ERR_UNSUPPORTED, "batch %lld or heads %lld exceed 65535", (long long)Bn,
@@ -718,6 +1005,18 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
   if ((rc = grid_for(Bn, H, P, p.vbpr_log2, grid)) != LQ_OK) return rc;
   const bool bcvec = bc_vector_ok(B) && bc_vector_ok(C);
   hipStream_t s = (hipStream_t)stream;
+  if (rows_path_ok(p, vec, bcvec, dt, dt_bias, A, D, round_mode, Bn * H * P * N)) {
+    p.lo_base = (uint32_t)(rng_offset >> 1);
+    p.kh = lowbias32_host((uint32_t)(rng_offset >> 33) ^ p.key);
+    const int rows = ROWS_PER_LANE * (256 >> p.vbpr_log2);
+    const dim3 rgrid((unsigned)((P + rows - 1) / rows), (unsigned)H, (unsigned)Bn);
+    if (format_bits == 8) {
+      dispatch_rows<8>(p, round_mode, rgrid, s);
+    } else {
+      dispatch_rows<4>(p, round_mode, rgrid, s);
+    }
+    return check_launch("lq_mx_state_update");
+  }
   if (format_bits == 8) {
     dispatch_update<8>(p, round_mode, vec, bcvec, grid, s);
   } else {

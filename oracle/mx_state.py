@@ -13,7 +13,13 @@ Encode of a block with absmax a (ms.py:168-203, 512-534, 557-571):
     level = round(qa)  (one of the modes below), min(level, M), negated when v < 0
 Rounding modes: nearest-even (torch.round, initial encode ms.py:568), half-up floor(qa + 0.5)
 (deterministic writeback ms.py:201, 482, 531), stochastic floor(qa) + (u < qa - floor(qa))
-(ms.py:196-199, 528-530) with u from a supplied tensor or from oracle.rng.
+(ms.py:196-199, 528-530) with u from a supplied tensor (ROUND_SR_UNIFORM, the reference's
+formula), and the counter mode ROUND_SR_COUNTER, which replaces the reference's Triton tl.rand
+draw by oracle.rng's 16-bit draws u16 used as a fixed-point dither:
+    T     = trunc(clamp(v * 2^16 / (base * 2^micro), -M*2^16, M*2^16))   (signed, one fp32 scaling)
+    level = floor((T + u16) / 2^16)
+which rounds |v| up with probability floor(frac(qa) * 2^16) / 2^16 (frac truncated to 16 bits,
+bias below 2^-16 of one step) on both signs, and never leaves [-M, M].
 
 ceil(log2(t)) is defined as the ceiling of the correctly rounded fp32 log2 of t. For a t with
 unbiased exponent E and mantissa field j, that ceiling is E when j == 0, E when the fp32 value
@@ -26,6 +32,8 @@ reachable E; ceil_log2 against exact integer comparisons away from the rounding 
 invariants (|q| <= M, e in [1, 254], micro in {0,1}); half-step error bound of the nearest-even
 decode; the all-zero block (e = 28, q = 0); exact powers of two; the floor(q + 0.5) double
 rounding case; stochastic rounding with u = 0 (ceil) and u -> 1 (floor) and its unbiasedness;
+the counter dither by enumerating all 2^16 draws (round-up count = floor(frac * 2^16) exactly,
+for both signs, exact fractions) and its clamp;
 the update's closed forms (dt = 0 leaves h unchanged so the writeback is a pure re-encode;
 A = 0 gives h + dt*B*x; softplus threshold at 20) against an independent float64 evaluation.
 bf16_state_update (drift baseline) restates mamba_ssm's selective_state_update, a dependency
@@ -86,9 +94,10 @@ def exp2_scale(biased: np.ndarray) -> np.ndarray:
 
 def mx_encode(state, format_bits: int, round_mode: int = ROUND_NEAREST_EVEN,
               uniform: np.ndarray | None = None, seed: int = 0,
-              rng_offset: int = 0) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+              rng_offset: int = 0, u16: np.ndarray | None = None
+              ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Encode a float state [..., N] -> (q int8 [..., N], shared_exp u8 [..., N/16],
-    micro_exp u8 [..., N/2])."""
+    micro_exp u8 [..., N/2]). `u16` overrides the counter draws of ROUND_SR_COUNTER."""
     if isinstance(state, torch.Tensor):
         state = state.detach().float().cpu().numpy()
     v = np.asarray(state, dtype=np.float32)
@@ -107,20 +116,32 @@ def mx_encode(state, format_bits: int, round_mode: int = ROUND_NEAREST_EVEN,
     micro = pair_amax > (m * base)[..., None]
     pair_scale = (base[..., None] * np.where(micro, np.float32(2.0), np.float32(1.0))).astype(
         np.float32)
+    if round_mode == ROUND_SR_COUNTER:
+        # fixed-point dither: T = v / pair_scale * 2^16 as one fp32 scaling (the pair scale is a
+        # power of two, 2^(se-127) with se = exponent + micro and exponent 127 for a zero block),
+        # clamped to +-M*2^16 and truncated toward zero; level = floor((T + u16) / 2^16).
+        se = np.where(amax == 0, 127, biased)[..., None] + micro.astype(np.int64)
+        t16 = np.ldexp(pairs, (143 - se)[..., None].astype(np.int32)).astype(np.float32)
+        t16 = np.clip(t16, -m * np.float32(65536.0), m * np.float32(65536.0))
+        if u16 is None:
+            u16 = rng.state_u16(seed, rng_offset, v.shape)
+        u16 = np.asarray(u16).reshape(pairs.shape).astype(np.int64)
+        level = (np.trunc(t16).astype(np.int64) + u16) >> 16
+        q = level.reshape(v.shape).astype(np.int8)
+        shared = biased.astype(np.uint8)
+        micro_u8 = micro.astype(np.uint8).reshape(*v.shape[:-1], n // PAIR)
+        return q, shared, micro_u8
     qa = np.minimum(np.abs(pairs) / pair_scale[..., None], m)
     if round_mode == ROUND_NEAREST_EVEN:
         level = np.rint(qa)
     elif round_mode == ROUND_HALF_UP:
         level = np.floor(qa + np.float32(0.5))
-    elif round_mode in (ROUND_SR_UNIFORM, ROUND_SR_COUNTER):
-        if round_mode == ROUND_SR_COUNTER:
-            u = rng.state_uniforms(seed, rng_offset, v.shape).reshape(pairs.shape)
-        else:
-            if uniform is None:
-                raise ValueError("ROUND_SR_UNIFORM needs a uniform tensor")
-            if isinstance(uniform, torch.Tensor):
-                uniform = uniform.detach().float().cpu().numpy()
-            u = np.asarray(uniform, dtype=np.float32).reshape(pairs.shape)
+    elif round_mode == ROUND_SR_UNIFORM:
+        if uniform is None:
+            raise ValueError("ROUND_SR_UNIFORM needs a uniform tensor")
+        if isinstance(uniform, torch.Tensor):
+            uniform = uniform.detach().float().cpu().numpy()
+        u = np.asarray(uniform, dtype=np.float32).reshape(pairs.shape)
         fl = np.floor(qa)
         level = fl + (u < (qa - fl)).astype(np.float32)
     else:

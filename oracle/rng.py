@@ -9,11 +9,11 @@ their own counter-based generator, restated here bit for bit:
     counter  = rng_offset + ((b*H + h)*P + p)*N + n                         (same offsets as above)
     pair     = counter >> 1,  half = counter & 1
     bits32   = lowbias32(lo32(pair) ^ lowbias32(hi32(pair) ^ K))
-    u        = ((bits32 >> (16*half)) & 0xFFFF) * 2^-16                     (16-bit uniform in [0,1))
+    u16      = (bits32 >> (16*half)) & 0xFFFF                               (16-bit uniform integer)
 
 lowbias32 is the 32-bit integer mixer x ^= x>>16; x *= 0x7feb352d; x ^= x>>15; x *= 0x846ca68b;
-x ^= x>>16 (C. Wellons, "hash prospector", public domain). A 16-bit uniform bounds the
-stochastic-rounding bias by 2^-16 of one quantization step.
+x ^= x>>16 (C. Wellons, "hash prospector", public domain). The even element of a pair takes the
+low half. oracle.mx_state uses u16 as a fixed-point dither (bias below 2^-16 of one step).
 
 Pinning (tests/test_oracle_mx.py): the vectorized numpy version against a scalar pure-Python
 version, known-answer vectors in tests/golden/rng_vectors.json, lowbias32 bijectivity on a
@@ -63,8 +63,8 @@ def uniform_scalar(seed: int, counter: int) -> float:
     return float((bits >> (16 * (counter & 1))) & 0xFFFF) / 65536.0
 
 
-def uniforms(seed: int, counters: np.ndarray) -> np.ndarray:
-    """Vectorized generator: counters (uint64 array) -> float32 uniforms in [0, 1)."""
+def uniforms_u16(seed: int, counters: np.ndarray) -> np.ndarray:
+    """Vectorized generator: counters (uint64 array) -> 16-bit uniform integers (uint32)."""
     c = np.asarray(counters, dtype=np.uint64)
     key = np.uint32(seed_key(seed))
     pair = c >> np.uint64(1)
@@ -72,12 +72,22 @@ def uniforms(seed: int, counters: np.ndarray) -> np.ndarray:
     hi = (pair >> np.uint64(32)).astype(np.uint32)
     bits = lowbias32(lo ^ lowbias32(hi ^ key))
     half = (c & np.uint64(1)).astype(np.uint32)
-    u16 = (bits >> (np.uint32(16) * half)) & np.uint32(0xFFFF)
-    return (u16.astype(np.float32) * np.float32(1.0 / 65536.0)).astype(np.float32)
+    return (bits >> (np.uint32(16) * half)) & np.uint32(0xFFFF)
+
+
+def uniforms(seed: int, counters: np.ndarray) -> np.ndarray:
+    """The same draws as float32 uniforms u16 * 2^-16 in [0, 1)."""
+    return (uniforms_u16(seed, counters).astype(np.float32) * np.float32(1.0 / 65536.0)).astype(
+        np.float32)
+
+
+def state_u16(seed: int, rng_offset: int, shape: tuple[int, ...]) -> np.ndarray:
+    """16-bit draws (uint32) for an MX state of `shape` = (B, H, P, N) at the given offset."""
+    n = int(np.prod(shape))
+    counters = np.uint64(rng_offset) + np.arange(n, dtype=np.uint64)
+    return uniforms_u16(seed, counters).reshape(shape)
 
 
 def state_uniforms(seed: int, rng_offset: int, shape: tuple[int, ...]) -> np.ndarray:
-    """Uniform tensor for an MX state of `shape` = (B, H, P, N) at the given offset."""
-    n = int(np.prod(shape))
-    counters = np.uint64(rng_offset) + np.arange(n, dtype=np.uint64)
-    return uniforms(seed, counters).reshape(shape)
+    """Float32 uniforms for an MX state of `shape` = (B, H, P, N) at the given offset."""
+    return (state_u16(seed, rng_offset, shape).astype(np.float32) * np.float32(1.0 / 65536.0))

@@ -86,20 +86,33 @@ def _assert_state_close(got, ref, rtol=2e-3):
     assert np.all(np.abs(g - w) <= bound * (1 + 1e-6)), "a value moved by more than one level"
 
 
-def _inputs(bsz, nh, p_, n, ng, seed, device, dt_zero=False):
+def _inputs(bsz, nh, p_, n, ng, seed, device, dt_zero=False, head_dt=False):
+    """Decode-step inputs. head_dt=True gives dt one value per (batch, head), expanded along
+    head_dim as Nemotron-H passes it: with the head-constant A, D and dt_bias below, that is the
+    layout the library's row kernel takes (the general kernel takes the rest)."""
     g = torch.Generator().manual_seed(seed)
+    dt_shape = (bsz, nh, 1) if head_dt else (bsz, nh, p_)
+    dt = torch.nn.functional.softplus(torch.randn(*dt_shape, generator=g)).to(torch.bfloat16)
+    if dt_zero:
+        dt = torch.zeros_like(dt)
     t = dict(
         x=torch.randn(bsz, nh, p_, generator=g).to(torch.bfloat16),
-        dt=torch.nn.functional.softplus(torch.randn(bsz, nh, p_, generator=g)).to(torch.bfloat16),
+        dt=dt.expand(bsz, nh, p_),
         A=(-torch.exp(torch.rand(nh, generator=g) * 2))[:, None, None].expand(nh, p_, n),
         B=torch.randn(bsz, ng, n, generator=g).to(torch.bfloat16),
         C=torch.randn(bsz, ng, n, generator=g).to(torch.bfloat16),
         D=torch.randn(nh, generator=g)[:, None].expand(nh, p_),
         dt_bias=(torch.randn(nh, generator=g) * 0.1)[:, None].expand(nh, p_),
     )
-    if dt_zero:
-        t["dt"] = torch.zeros_like(t["dt"])
     return {k: v.to(device) for k, v in t.items()}
+
+
+@pytest.fixture(params=["rows", "general"])
+def path(request, monkeypatch):
+    """Run a test on the row kernel's layout, and once more with the general kernel forced."""
+    if request.param == "general":
+        monkeypatch.setenv("LQ_MX_FORCE_GENERIC", "1")
+    return request.param
 
 
 def _cpu(t):
@@ -107,12 +120,12 @@ def _cpu(t):
 
 
 @pytest.mark.parametrize("fb", [8, 4])
-@pytest.mark.parametrize("mode", [1, 2, 3])
-def test_update_dt_zero_writeback_bit_exact(gpu, fb, mode):
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+def test_update_dt_zero_writeback_bit_exact(gpu, path, fb, mode):
     shape = (2, 16, 8, 128)
     h0 = _state(shape, 30 + fb)
     q, e, m = omx.mx_encode(h0.numpy(), fb, 0)
-    t = _inputs(2, 16, 8, 128, 2, 31, gpu, dt_zero=True)
+    t = _inputs(2, 16, 8, 128, 2, 31, gpu, dt_zero=True, head_dt=True)
     uni = torch.rand(shape, generator=torch.Generator().manual_seed(32))
     st = [torch.from_numpy(a).to(gpu) for a in (q, e, m)]
     out = torch.empty(2, 16, 8, device=gpu)
@@ -130,12 +143,13 @@ def test_update_dt_zero_writeback_bit_exact(gpu, fb, mode):
 
 @pytest.mark.parametrize("fb", [8, 4])
 @pytest.mark.parametrize("softplus", [True, False])
-def test_update_parity(gpu, fb, softplus):
+@pytest.mark.parametrize("head_dt", [True, False])
+def test_update_parity(gpu, fb, softplus, head_dt):
     bsz, nh, p_, n, ng = 4, 32, 16, 128, 4
     shape = (bsz, nh, p_, n)
     h0 = _state(shape, 40 + fb)
     q, e, m = omx.mx_encode(h0.numpy(), fb, 0)
-    t = _inputs(bsz, nh, p_, n, ng, 41, gpu)
+    t = _inputs(bsz, nh, p_, n, ng, 41, gpu, head_dt=head_dt)
     z = torch.randn(bsz, nh, p_, generator=torch.Generator().manual_seed(42)).to(gpu)
     uni = torch.rand(shape, generator=torch.Generator().manual_seed(43))
     st = [torch.from_numpy(a).to(gpu) for a in (q, e, m)]
@@ -180,6 +194,48 @@ def test_update_general_A_and_strides(gpu):
 
 
 @pytest.mark.parametrize("fb", [8, 4])
+@pytest.mark.parametrize("n", [64, 96, 128, 256])
+def test_update_counter_mode_nonzero_dt(gpu, path, fb, n):
+    """Counter-mode writeback after a real update on the row kernel's layout (d_state 64, 128,
+    256, and 96 on the general kernel): y within 2e-3, the state within 2e-3 with at most
+    one-level flips; P = 40 leaves a partly filled last row group."""
+    bsz, nh, p_, ng = 2, 8, 40, 2
+    shape = (bsz, nh, p_, n)
+    h0 = _state(shape, 90 + fb + n)
+    q, e, m = omx.mx_encode(h0.numpy(), fb, 0)
+    t = _inputs(bsz, nh, p_, n, ng, 91, gpu, head_dt=True)
+    st = [torch.from_numpy(a).to(gpu) for a in (q, e, m)]
+    out = torch.empty(bsz, nh, p_, device=gpu)
+    off = 16 * 12345
+    _abi.mx_state_update(*st, t["x"], t["dt"], t["dt_bias"], t["A"], t["B"], t["C"], t["D"], None,
+                         out, fb, True, 3, seed=5, rng_offset=off)
+    c = _cpu(t)
+    rq, re_, rm, ry, _ = omx.mx_update(q, e, m, c["x"], c["dt"], c["A"], c["B"], c["C"], D=c["D"],
+                                       dt_bias=c["dt_bias"], dt_softplus=True, format_bits=fb,
+                                       round_mode=3, seed=5, rng_offset=off)
+    assert_close_rel(out.cpu(), ry, what="y")
+    _assert_state_close([a.cpu().numpy() for a in st], (rq, re_, rm))
+
+
+@pytest.mark.parametrize("off", [2**33 - 8192, 16 * 999 + 2])
+def test_update_counter_offsets_general_kernel(gpu, off):
+    """Offsets the row kernel declines (pair counters crossing 2^32 inside the launch; an offset
+    not a multiple of 16) go to the general kernel: still bit-exact with dt = 0."""
+    shape = (2, 8, 8, 128)
+    h0 = _state(shape, 95)
+    q, e, m = omx.mx_encode(h0.numpy(), 4, 0)
+    t = _inputs(2, 8, 8, 128, 2, 96, gpu, dt_zero=True, head_dt=True)
+    st = [torch.from_numpy(a).to(gpu) for a in (q, e, m)]
+    out = torch.empty(2, 8, 8, device=gpu)
+    _abi.mx_state_update(*st, t["x"], t["dt"], None, t["A"], t["B"], t["C"], None, None, out, 4,
+                         False, 3, seed=6, rng_offset=off)
+    c = _cpu(t)
+    rq, re_, rm, _, _ = omx.mx_update(q, e, m, c["x"], c["dt"], c["A"], c["B"], c["C"],
+                                      format_bits=4, round_mode=3, seed=6, rng_offset=off)
+    _assert_mx_equal(st, (rq, re_, rm))
+
+
+@pytest.mark.parametrize("fb", [8, 4])
 def test_counter_chain_module_api(gpu, fb):
     """allocate_state_kernel_cache + 5 chained updates with dt = 0 (pure re-encodes at rising
     counter offsets) stay bit-exact with the oracle chain."""
@@ -188,7 +244,7 @@ def test_counter_chain_module_api(gpu, fb):
     cache = ms.allocate_state_kernel_cache(h0.to(gpu), format_bits=fb)
     ref = omx.mx_encode(h0.float().numpy(), fb, 0)
     _assert_mx_equal((cache.q_state, cache.shared_exp, cache.micro_exp), ref)
-    t = _inputs(2, 8, 4, 128, 2, 61, gpu, dt_zero=True)
+    t = _inputs(2, 8, 4, 128, 2, 61, gpu, dt_zero=True, head_dt=True)
     c = _cpu(t)
     for step in range(5):
         y = ms.mx_state_selective_update(cache, t["x"], t["dt"], t["A"], t["B"], t["C"],
@@ -209,8 +265,8 @@ def test_counter_chain_module_api(gpu, fb):
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("fb", [4])
 def test_full_size_b64_dt_zero_bit_exact(gpu, fb):
-    """BASELINE size (B=64, 128 heads x 64 x 128): counter-generator writeback bit-exact.
-    (The numpy oracle needs about a minute here.)"""
+    """Headline size (B=64, 128 heads x 64 x 128, the model's layout): counter-mode writeback
+    bit-exact. (The numpy oracle needs about a minute here.)"""
     shape = (64, 128, 64, 128)
     gen = torch.Generator(device=gpu).manual_seed(70 + fb)
     h0 = torch.randn(shape, device=gpu, generator=gen) * 0.5
@@ -218,7 +274,7 @@ def test_full_size_b64_dt_zero_bit_exact(gpu, fb):
     _abi.mx_encode(h0, *st, fb, 0)
     q0, e0, m0 = (a.cpu().numpy() for a in st)
     x = torch.randn(64, 128, 64, device=gpu, generator=gen).to(torch.bfloat16)
-    dt = torch.zeros(64, 128, 64, device=gpu, dtype=torch.bfloat16)
+    dt = torch.zeros(64, 128, 1, device=gpu, dtype=torch.bfloat16).expand(64, 128, 64)
     A = (-torch.rand(128, device=gpu, generator=gen))[:, None, None].expand(128, 64, 128)
     B = torch.randn(64, 8, 128, device=gpu, generator=gen).to(torch.bfloat16)
     C = torch.randn(64, 8, 128, device=gpu, generator=gen).to(torch.bfloat16)

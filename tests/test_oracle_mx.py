@@ -113,6 +113,49 @@ def test_stochastic_rounding_extremes_and_unbiasedness():
     assert bias.mean() < 0.03 and bias.max() < 0.2
 
 
+def test_counter_dither_enumerates_to_the_truncated_fraction():
+    """All 2^16 draws for one value: the round-up count is floor(frac(qa) * 2^16), exactly, on
+    both signs; the pair (7, x) of a block with absmax 7 has scale 1, so qa = |x|."""
+    u = np.arange(1 << 16, dtype=np.uint32)
+    for x in (2.3, 0.7, 6.99999, 1.0 + 2.0**-20, 5.0, 0.0, 3.0 + 2.0**-16 + 2.0**-17):
+        for sign in (1.0, -1.0):
+            xv = np.float32(sign * x)
+            v = np.zeros((u.size, 16), np.float32)
+            v[:, 0] = 7.0
+            v[:, 1] = xv
+            draws = np.zeros(v.shape, np.uint32)
+            draws[:, 1] = u
+            q, e, m = mx.mx_encode(v, 4, mx.ROUND_SR_COUNTER, u16=draws)
+            assert (e == 126).all() and (m[:, 0] == 1).all()
+            mag = Fraction(float(abs(xv)))
+            fl = int(mag)
+            want_up = int((mag - fl) * 65536)
+            lv = np.abs(q[:, 1].astype(np.int64))
+            assert set(np.unique(lv)) <= {fl, fl + 1}
+            assert int((lv == fl + 1).sum()) == want_up, (x, sign)
+            if xv != 0:
+                assert (np.sign(q[:, 1][lv > 0]) == np.sign(xv)).all()
+
+
+def test_counter_dither_clamps_at_the_mantissa_limit():
+    """A block whose rounded absmax/14 sits 20 ulps above 2^-80 keeps e = -80 (inside the
+    correctly rounded log2 band), so the micro pair's qa = 7 + 140*2^-23 exceeds M = 7 by more
+    than 2^-16: without the clamp the largest draws would give level 8."""
+    amax = np.float32(2.0**-77 * (1.75 + 35 * 2.0**-23))
+    assert float(amax) / 14 == 2.0**-80 * (1 + 20 * 2.0**-23)
+    u = np.arange(1 << 16, dtype=np.uint32)
+    for sign in (1.0, -1.0):
+        v = np.zeros((u.size, 16), np.float32)
+        v[:, 0] = sign * amax
+        draws = np.zeros(v.shape, np.uint32)
+        draws[:, 0] = u
+        q, e, m = mx.mx_encode(v, 4, mx.ROUND_SR_COUNTER, u16=draws)
+        assert (e == 127 - 80).all() and (m[:, 0] == 1).all()
+        assert (q[:, 0] == int(sign * 7)).all()
+    t16 = Fraction(float(amax)) * 2**79 * 65536
+    assert (int(t16) + 65535) >> 16 == 8
+
+
 def _independent_update(h, x, dt, A, B, C, D, z, dt_bias, softplus):
     """float64 loop over heads, written without the oracle's broadcasting."""
     bsz, nh, p_, n = h.shape
