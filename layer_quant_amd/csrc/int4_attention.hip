@@ -123,33 +123,56 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(AttnParams p) {
 
 // Combines the split partials of one (batch, query head): M = max m_s, w_s = 2^(m_s - M),
 // out = sum w_s acc_s / sum w_s l_s. A split with m_s = -inf (all keys masked) has weight 0.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// One wave per (batch, query head): M = max_s m_s and L = sum_s 2^(m_s - M) l_s from
+// lane-parallel loads and wave reductions, then out = sum_s 2^(m_s - M) acc_s / L with the
+// per-split partial rows loaded four splits at a time.
 __global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams p) {
   const int lane = threadIdx.x;
   const int bh = blockIdx.x;
   const int b = bh / p.Hq;
   const int qh = bh - b * p.Hq;
   const int64_t base = (int64_t)bh * p.nsplit;
+  const int ns = p.nsplit;
   float M = -INFINITY;
-  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, p.ws_m[base + s]);
+  for (int s = lane; s < ns; s += 64) M = fmaxf(M, p.ws_m[base + s]);
+  M = wave_max(M);
   float L = 0.0f;
+  for (int s = lane; s < ns; s += 64) {
+    const float ms = p.ws_m[base + s];
+    L += (ms == -INFINITY) ? 0.0f : exp2f(ms - M) * p.ws_l[base + s];
+  }
+  L = wave_sum(L);
+  const int nd = (p.D + 63) >> 6;
   float acc[GEN_MAX_D / 64];
 #pragma unroll
   for (int i = 0; i < GEN_MAX_D / 64; ++i) acc[i] = 0.0f;
-  for (int s = 0; s < p.nsplit; ++s) {
+#pragma unroll 4
+  for (int s = 0; s < ns; ++s) {
     const float ms = p.ws_m[base + s];
     const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
-    L += w * p.ws_l[base + s];
     const float* a = p.ws_acc + (base + s) * p.D;
 #pragma unroll
     for (int i = 0; i < GEN_MAX_D / 64; ++i) {
       const int d = lane + 64 * i;
-      if (d < p.D) acc[i] += w * a[d];
+      if (i < nd && d < p.D) acc[i] += w * a[d];
     }
   }
 #pragma unroll
   for (int i = 0; i < GEN_MAX_D / 64; ++i) {
     const int d = lane + 64 * i;
-    if (d < p.D) {
+    if (i < nd && d < p.D) {
       store_float(p.out.data, p.out.dtype, b * p.out.s[0] + qh * p.out.s[1] + d * p.out.s[2],
                   acc[i] / L);
     }

@@ -468,12 +468,31 @@ bool fast_path_ok(const AttnParams& p) {
   return true;
 }
 
+// Waves of attn_fast_kernel resident on the current device at once: its register use (over 128
+// VGPRs) leaves 2 waves per SIMD, 4 SIMDs per CU.
+static int64_t resident_fast_waves() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 2048;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0) {
+      cus = 256;
+    }
+    cached[dev] = cus * 4 * 2;
+  }
+  return cached[dev];
+}
+
 SplitPlan plan_fast(int64_t B, int64_t Hkv, int64_t S) {
-  // about 16K waves: keys per wave rounded to the 32-key tile, 4 waves per workgroup split
-  const int64_t target_waves = 16384;
+  // One resident generation of waves: each wave walks as many keys as that takes (rounded to the
+  // 32-key tile, 4 waves per workgroup split). Fewer, longer waves amortize the per-wave setup
+  // and the 4-wave merge, and at B * Hkv >= resident / 4 no split-K merge runs at all.
+  const int64_t target_waves = resident_fast_waves();
   int64_t tpw = (B * Hkv * S + target_waves - 1) / target_waves;
   tpw = ((tpw + TILE - 1) / TILE) * TILE;
-  tpw = std::min<int64_t>(std::max<int64_t>(tpw, TILE), 1024);
+  tpw = std::min<int64_t>(std::max<int64_t>(tpw, TILE), (int64_t)1 << 20);
   SplitPlan sp{};
   sp.chunk = WAVES * tpw;
   sp.nsplit = (int)std::max<int64_t>(1, (S + sp.chunk - 1) / sp.chunk);

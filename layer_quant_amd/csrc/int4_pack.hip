@@ -3,8 +3,9 @@
 // Replaces _pack_int4_kv_kernel (reference hybrid_quant/int4_8b_attention.py:32-111). Per group
 // of g values along head_dim: absmax -> scale = max(absmax / 7, 1e-8) -> q = rint(x / scale)
 // (IEEE division, round half to even) -> clamp [-8, 7] -> two's-complement nibbles, even d in the
-// low nibble. One thread owns one (batch, kv-head, token, group); decode writes one token per
-// call, so the kernel is launch-bound and kept simple.
+// low nibble. int4_pack_lanes_kernel gives one lane to each output byte (dims 2j, 2j+1), so a
+// group is g/2 adjacent lanes and its absmax a shuffle reduction; int4_pack_kernel (one thread
+// per group) covers group sizes whose g/2 is not a power of two up to 64.
 #include "lq_common.h"
 
 namespace lq {
@@ -20,6 +21,39 @@ struct PackParams {
   int B, H, T, D, g;
   int64_t cap;
 };
+
+// One lane per packed byte; GH = g/2 lanes per group (a power of two <= 64, so groups never
+// straddle a wave). Lane offsets are 32-bit (the host checks the element count).
+template <int GH>
+__global__ __launch_bounds__(256) void int4_pack_lanes_kernel(PackParams p) {
+  const int half = p.D >> 1;
+  const int total = p.B * p.H * p.T * half;
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  const bool in = gid < total;
+  const int g2 = in ? gid : total - 1;  // whole trailing groups only; they store nothing
+  const int j = g2 % half;
+  const int row = g2 / half;
+  const int t = row % p.T;
+  const int bh = row / p.T;
+  const int h = bh % p.H;
+  const int b = bh / p.H;
+  const int64_t xrow = b * p.x.s[0] + h * p.x.s[1] + t * p.x.s[2];
+  const float v0 = load_float(p.x.data, p.x.dtype, xrow + (2 * j) * p.x.s[3]);
+  const float v1 = load_float(p.x.data, p.x.dtype, xrow + (2 * j + 1) * p.x.s[3]);
+  float amax = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+  for (int o = GH >> 1; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  const float scale = fmaxf(amax / 7.0f, 1.0e-8f);
+  const int q0 = min(max((int)rintf(v0 / scale), -8), 7);
+  const int q1 = min(max((int)rintf(v1 / scale), -8), 7);
+  const int64_t pos = p.positions[t * p.pos_stride];
+  if (!in || pos < 0 || pos >= p.cap) return;
+  p.packed[b * p.ps[0] + h * p.ps[1] + pos * p.ps[2] + j * p.ps[3]] =
+      (uint8_t)(((q1 & 15) << 4) | (q0 & 15));
+  if ((j & (GH - 1)) == 0) {
+    p.scale[b * p.ss[0] + h * p.ss[1] + pos * p.ss[2] + (j / GH) * p.ss[3]] = scale;
+  }
+}
 
 __global__ __launch_bounds__(256) void int4_pack_kernel(PackParams p) {
   const int groups = p.D / p.g;
@@ -108,10 +142,25 @@ extern "C" int lq_int4_pack_kv(const lq_tensor* x, const lq_tensor* packed,
   p.D = (int)D;
   p.g = group_size;
   p.cap = cap;
+  hipStream_t s = (hipStream_t)stream;
+  const int gh = group_size / 2;
+  const int64_t bytes = B * H * T * (D / 2);
+  if (gh <= 64 && (gh & (gh - 1)) == 0 && bytes < ((int64_t)1 << 31) - 256) {
+    const dim3 grid((unsigned)((bytes + 255) / 256));
+    switch (gh) {
+      case 1: hipLaunchKernelGGL(int4_pack_lanes_kernel<1>, grid, dim3(256), 0, s, p); break;
+      case 2: hipLaunchKernelGGL(int4_pack_lanes_kernel<2>, grid, dim3(256), 0, s, p); break;
+      case 4: hipLaunchKernelGGL(int4_pack_lanes_kernel<4>, grid, dim3(256), 0, s, p); break;
+      case 8: hipLaunchKernelGGL(int4_pack_lanes_kernel<8>, grid, dim3(256), 0, s, p); break;
+      case 16: hipLaunchKernelGGL(int4_pack_lanes_kernel<16>, grid, dim3(256), 0, s, p); break;
+      case 32: hipLaunchKernelGGL(int4_pack_lanes_kernel<32>, grid, dim3(256), 0, s, p); break;
+      default: hipLaunchKernelGGL(int4_pack_lanes_kernel<64>, grid, dim3(256), 0, s, p); break;
+    }
+    return check_launch("lq_int4_pack_kv");
+  }
   const int64_t total = B * H * T * (D / group_size);
   const int threads = 256;
   const int64_t blocks = (total + threads - 1) / threads;
-  hipLaunchKernelGGL(int4_pack_kernel, dim3((unsigned)blocks), dim3(threads), 0,
-                     (hipStream_t)stream, p);
+  hipLaunchKernelGGL(int4_pack_kernel, dim3((unsigned)blocks), dim3(threads), 0, s, p);
   return check_launch("lq_int4_pack_kv");
 }

@@ -38,6 +38,22 @@ def test_pack_bit_exact(gpu, g, dtype):
     assert torch.equal(scale.cpu(), ref_s)
 
 
+@pytest.mark.parametrize("g,d", [(48, 96), (6, 96), (256, 256)])
+def test_pack_bit_exact_other_groups(gpu, g, d):
+    """Groups whose g/2 is not a power of two up to 64 take the one-thread-per-group kernel."""
+    b, h, t, cap = 2, 3, 4, 16
+    x = _activations((b, h, t, d), 200 + g)
+    pos = torch.tensor([3, 0, 15, 9])
+    packed = torch.full((b, h, cap, d // 2), 0xAB, dtype=torch.uint8, device=gpu)
+    scale = torch.full((b, h, cap, d // g), -1.0, device=gpu)
+    _abi.int4_pack_kv(x.to(gpu), packed, scale, pos.to(gpu), g)
+    ref_p = torch.full((b, h, cap, d // 2), 0xAB, dtype=torch.uint8)
+    ref_s = torch.full((b, h, cap, d // g), -1.0)
+    oik.pack_into(ref_p, ref_s, x, pos, g)
+    assert torch.equal(packed.cpu(), ref_p)
+    assert torch.equal(scale.cpu(), ref_s)
+
+
 def test_pack_edge_values(gpu):
     d, g = 128, 32
     x = torch.zeros(1, 1, 4, d)
