@@ -172,12 +172,14 @@ def cpu_baseline(args):
     torch.set_num_threads(cores)
     gen = torch.Generator().manual_seed(0)
     hq, hkv, d, g = 32, 8, 128, args.group
-    s_sample = min(args.ctx, 4096)
-    cache = oik.allocate_cache(1, hkv, s_sample, d, g)
-    kv = torch.randn(1, hkv, s_sample, d, generator=gen).to(torch.bfloat16)
+    s_sample = args.ctx
+    ba_sample = min(args.batch, 2)
+    cache = oik.allocate_cache(ba_sample, hkv, s_sample, d, g)
+    kv = torch.randn(ba_sample, hkv, s_sample, d, generator=gen).to(torch.bfloat16)
     oik.pack_kv_into_cache(cache, kv, kv, torch.arange(s_sample), g)
-    q = torch.randn(1, hq, 1, d, generator=gen).to(torch.bfloat16)
-    new = torch.randn(1, hkv, 1, d, generator=gen).to(torch.bfloat16)
+    del kv
+    q = torch.randn(ba_sample, hq, 1, d, generator=gen).to(torch.bfloat16)
+    new = torch.randn(ba_sample, hkv, 1, d, generator=gen).to(torch.bfloat16)
 
     def attn_once():
         oik.pack_into(cache["k_packed"], cache["k_scale"], new, torch.tensor([s_sample - 1]), g)
@@ -185,7 +187,7 @@ def cpu_baseline(args):
         oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
                              cache["v_scale"], s_sample, 4, g)
 
-    b_sample = 2
+    b_sample = min(args.batch, 8)
     shape = (b_sample, 128, 64, 128)
     qs, es, ms_ = omx.mx_encode((torch.randn(shape, generator=gen) * 0.5).numpy(), args.state_bits)
     x = torch.randn(b_sample, 128, 64, generator=gen).to(torch.bfloat16)
@@ -207,9 +209,10 @@ def cpu_baseline(args):
             ts.append(time.perf_counter() - t0)
         return float(np.median(ts))
 
-    t_attn = timed(attn_once, 3)
-    t_mx = timed(mx_once, 3)
-    scale_attn = args.batch * (args.ctx / s_sample)
+    reps = 3
+    t_attn = timed(attn_once, reps)
+    t_mx = timed(mx_once, reps)
+    scale_attn = (args.batch / ba_sample) * (args.ctx / s_sample)
     scale_mx = args.batch / b_sample
     step_s = args.attn_layers * t_attn * scale_attn + args.mamba_layers * t_mx * scale_mx
     return {
@@ -217,11 +220,13 @@ def cpu_baseline(args):
         "unit": "us/step",
         "cores": cores,
         "kind": "port",
-        "sample": (f"oracle (torch/numpy CPU) on 1 attention layer at batch 1, ctx {s_sample} "
+        "sample": (f"oracle (torch/numpy CPU, torch threads = cores; numpy elementwise work "
+                   f"single-threaded) on 1 attention layer at batch {ba_sample}, ctx {s_sample} "
                    f"(pack K,V + attend) and 1 MX{args.state_bits} update at batch {b_sample}, "
-                   f"median of 3, scaled linearly to {args.attn_layers} layers x batch "
-                   f"{args.batch} x ctx {args.ctx} and {args.mamba_layers} layers x batch "
-                   f"{args.batch}; attention {t_attn * 1e3:.1f} ms, update {t_mx * 1e3:.1f} ms"),
+                   f"median of {reps} after one warm-up, scaled linearly to {args.attn_layers} "
+                   f"layers x batch {args.batch} x ctx {args.ctx} and {args.mamba_layers} layers x "
+                   f"batch {args.batch}; attention {t_attn * 1e3:.1f} ms, update "
+                   f"{t_mx * 1e3:.1f} ms per sample call"),
     }
 
 
@@ -293,8 +298,9 @@ def main():
     dk = kernels[dominant]
     workload = f"b{args.batch}_ctx{args.ctx}_g{args.group}_mx{args.state_bits}"
     roofline = {
-        "kernel": {"attention": "lq_int4_decode_attention (attn_fast_kernel + attn_merge_kernel)",
-                   "mx_update": f"lq_mx_state_update (mx_update_kernel MX{args.state_bits})",
+        "kernel": {"attention": "lq_int4_decode_attention (attn_fast_kernel, + attn_merge_kernel "
+                                "when split)",
+                   "mx_update": f"lq_mx_state_update (mx_update_rows_kernel MX{args.state_bits})",
                    "pack": "lq_int4_pack_kv"}[dominant],
         "bound": "hbm",
         "achieved": dk["GB_s"],
