@@ -47,6 +47,10 @@ struct MxUpdateParams {
   // rows kernel, counter mode: hash of the pair counters' common high word, and the low word of
   // rng_offset / 2 (the launch's pair counters share one high word)
   uint32_t kh, lo_base;
+  // rows kernel: byte stride between rows of x, z and out, and the byte span of one
+  // (batch, head) slice of each rounded up to 4 (0 for an absent z)
+  uint32_t x_row_bytes, z_row_bytes, out_row_bytes;
+  uint32_t x_span, z_span, out_span;
 };
 
 struct MxCodecParams {
@@ -178,6 +182,57 @@ __device__ __forceinline__ bool block_exponent(float amax, int& eb, int& ebase) 
   return band;
 }
 
+// block_exponent with a fast path. For absmax in [2^-92, 2^120), q = RN(absmax * RN(1/2M)) lies
+// within 2 ulps of t = RN(absmax / 2M) (q = (absmax/2M)(1 + d)(1 + f), |d|, |f| <= 2^-24); when
+// q's mantissa field is in [48, 2^23 - 4], t is in q's binade, more than 44 ulps above its power
+// of two, and t > 1e-30, so eb = E(q) + 128 with no clamp (eb in [29, 245]) and no band. Other
+// blocks take the exact rule. (Checked against block_exponent for every positive fp32 absmax.)
+constexpr uint32_t FAST_AMAX_LO = 0x11800000u;  // 2^-92
+constexpr uint32_t FAST_AMAX_HI = 0x7b800000u;  // 2^120
+constexpr uint32_t FAST_MANT_LO = 48u;
+constexpr uint32_t FAST_MANT_HI = 0x7ffffcu;
+
+template <int FB>
+__device__ __forceinline__ bool block_exponent_fast(float amax, int& eb, int& ebase) {
+  constexpr float C = FB == 8 ? 1.0f / 126.0f : 1.0f / 14.0f;
+  const uint32_t qb = __float_as_uint(amax * C);
+  const bool fast = (__float_as_uint(amax) - FAST_AMAX_LO) < (FAST_AMAX_HI - FAST_AMAX_LO) &&
+                    ((qb & 0x7fffffu) - FAST_MANT_LO) <= (FAST_MANT_HI - FAST_MANT_LO);
+  if (__builtin_expect(fast, 1)) {
+    eb = (int)(qb >> 23) + 1;
+    ebase = eb;
+    return false;
+  }
+  return block_exponent<FB>(amax, eb, ebase);
+}
+
+// max(|a|, |b|) and max(a, b, c) as single instructions: the operands are arithmetic results
+// (never signalling NaNs), so the canonicalising moves the compiler adds for fmaxf are not needed.
+__device__ __forceinline__ float abs_max2(float a, float b) {
+  float r;
+  asm("v_max_f32_e64 %0, |%1|, |%2|" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max_with_zero(float a, float b) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// Pair maxima and the block absmax of 16 values, max(0, |v_0|, ..., |v_15|) with NaNs ignored
+// (IEEE maxNum), as a running fmaxf from 0 gives.
+__device__ __forceinline__ float pair_maxima(const float (&v)[16], float (&pa)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) pa[k] = abs_max2(v[2 * k], v[2 * k + 1]);
+  const float m = max3(max3(pa[0], pa[1], pa[2]), pa[3], pa[4]);
+  return max_with_zero(max3(m, pa[5], pa[6]), pa[7]);
+}
+
 // Encode 16 values in the nearest-even, half-up or supplied-uniform mode. `u16` holds the
 // supplied uniforms scaled by 2^16 (so that the comparison u < frac becomes u16 < frac * 2^16,
 // both sides exact), unused otherwise. The reference's final min(level, M) is omitted: every mode
@@ -188,14 +243,9 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16
 #pragma clang fp contract(off)
   constexpr float M = FB == 8 ? 63.0f : 7.0f;
   float pa[8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    pa[k] = fmaxf(fabsf(v[2 * k]), fabsf(v[2 * k + 1]));
-    amax = fmaxf(amax, pa[k]);
-  }
+  const float amax = pair_maxima(v, pa);
   int eb, ebase;
-  block_exponent<FB>(amax, eb, ebase);
+  block_exponent_fast<FB>(amax, eb, ebase);
   const float thr = M * __uint_as_float((uint32_t)ebase << 23);
   // exact reciprocals of the pair scales 2^(se-127), se = ebase + micro: normal for se <= 253,
   // the subnormal 2^-127 for se = 254, and 0 for se = 255 (scale +inf; only reachable when
@@ -251,14 +301,9 @@ __device__ __forceinline__ void encode16_dither(const float (&v)[16], const uint
   constexpr float M = FB == 8 ? 63.0f : 7.0f;
   constexpr float MT = M * 65536.0f;
   float pa[8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    pa[k] = fmaxf(fabsf(v[2 * k]), fabsf(v[2 * k + 1]));
-    amax = fmaxf(amax, pa[k]);
-  }
+  const float amax = pair_maxima(v, pa);
   int eb, ebase;
-  const bool band = block_exponent<FB>(amax, eb, ebase);
+  const bool band = block_exponent_fast<FB>(amax, eb, ebase);
   const float thr = M * __uint_as_float((uint32_t)ebase << 23);
   const int sh0 = 143 - ebase;
   const int sh1 = sh0 - 1;
@@ -505,101 +550,152 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
-// Row kernel geometry: 256 threads, 2 rows per lane, so 2 * 256 / (N/16) rows per workgroup
-// (64 = one Nemotron-H head at N = 128).
-constexpr int ROWS_PER_LANE = 2;
-template <int BPR_LOG2>
-constexpr int rows_per_group() { return ROWS_PER_LANE * (256 >> BPR_LOG2); }
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, BUF_DWORD3);
+}
+
+// Float value of the 16- or 32-bit element held in the 32-bit word w at bit `shift` (0 or 16).
+__device__ __forceinline__ float word_elem(uint32_t w, uint32_t shift, int dtype) {
+  const uint32_t h16 = (w >> shift) & 0xffffu;
+  if (dtype == LQ_F32) return __uint_as_float(w);
+  if (dtype == LQ_BF16) return __uint_as_float(h16 << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+// Element at a wave-uniform address, read by a scalar load of the aligned 32-bit word holding it
+// (a 4-byte aligned word never crosses a page, so it stays inside the allocation's pages).
+__device__ __forceinline__ float uniform_elem(const char* addr, int dtype) {
+  typedef const __attribute__((address_space(4))) uint32_t* cword_t;
+  const uintptr_t a = (uintptr_t)addr;
+  const uint32_t w = *(cword_t)(a & ~(uintptr_t)3);
+  return word_elem(w, (uint32_t)(a & 2u) * 8u, dtype);
+}
 
 // Update of the model's decode call (ms.py:97-222, 289-544 for the Nemotron-H layout): state rows
 // contiguous (row stride N), B and C bf16 with a contiguous d_state, and dt, dt_bias, A and D
 // constant within a head (stride 0 along head_dim, A also along d_state), as the model passes
-// them. Grid (ceil(P / rows_per_group), H, B), 256 threads; lane (slot, blk) owns block column
-// blk of rows slot and slot + SLOTS (SLOTS = 256 / (N/16)), so B*dt and C are decoded once for two
-// rows, and every wave load covers 1 KB of consecutive state rows. Same arithmetic as mx_update_kernel in the (B*dt)*x order; in
-// the counter mode rng_offset is a multiple of 16, so a block's pair counters are lo0 | k and
-// lowbias32's first step folds into one per-block word.
-template <int FB, int RMODE, int BPR_LOG2>
-__global__ __launch_bounds__(256) void mx_update_rows_kernel(MxUpdateParams p) {
+// them. Grid (ceil(P / (R * SLOTS)), H, B), THREADS threads; lane (slot, blk) owns block column
+// blk of rows slot + r * SLOTS (r < R, SLOTS = THREADS / (N/16)), so B*dt and C are decoded once
+// for R rows, and every wave load covers consecutive state rows.
+// Every load of a lane (R state blocks, R x values, B, C, the head scalars) is issued before the
+// first use of any of them; all lane offsets are 32-bit offsets into per-(batch, head) buffer
+// descriptors. Same arithmetic as mx_update_kernel in the (B*dt)*x order; in the counter mode
+// rng_offset is a multiple of 16, so a block's pair counters are lo0 | k and lowbias32's first
+// step folds into one per-block word.
+template <int FB, int RMODE, int BPR_LOG2, int R, int THREADS>
+__global__ __launch_bounds__(THREADS) void mx_update_rows_kernel(MxUpdateParams p) {
   constexpr int BPR = 1 << BPR_LOG2;
-  constexpr int N = 16 * BPR;
-  constexpr int R = ROWS_PER_LANE;
-  constexpr int SLOTS = 256 >> BPR_LOG2;
+  constexpr uint32_t N = 16 * BPR;
+  constexpr int SLOTS = THREADS >> BPR_LOG2;
   const int h = blockIdx.y, b = blockIdx.z;
   const int blk = threadIdx.x & (BPR - 1);
   const int slot = threadIdx.x >> BPR_LOG2;
-  const int n0 = blk * 16;
+  const uint32_t n0 = (uint32_t)blk * 16u;
+  const int P = p.P;
 
-  int8_t* qb = p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1] + n0;
-  uint8_t* mb = p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1] + blk * 8;
-  uint8_t* eb = p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1] + blk;
-  const char* xb = vbase(p.x, b, h);
-  int pp[R];
-  bool act[R];
-  uint32_t qw[R][4], mw[R][2], ev[R];
-  float xv[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    pp[r] = blockIdx.x * rows_per_group<BPR_LOG2>() + r * SLOTS + slot;
-    act[r] = pp[r] < p.P;
-    const int pc = act[r] ? pp[r] : p.P - 1;
-    load_block<true>(qb + pc * N, mb + pc * (N / 2), eb + pc * (N / 16), qw[r], mw[r], ev[r]);
-    xv[r] = ldf(xb, p.x.dtype, __umul24(pc, (uint32_t)p.x.s[2]));
-  }
-
-  // head scalars (ms.py:134-139); exp and log use the hardware transcendentals (relative error
-  // ~1e-6, far inside the 2e-3 output tolerance)
-  float dtv = ldf(vbase(p.dt, b, h), p.dt.dtype, 0);
-  if (p.has_dtb) dtv += ldf(vbase(p.dtb, h, 0), p.dtb.dtype, 0);
-  if (p.softplus) dtv = dtv <= 20.0f ? __logf(1.0f + __expf(dtv)) : dtv;
-  const float dA = __expf(ldf(vbase(p.A, h, 0), p.A.dtype, 0) * dtv);
-  const float Dh = p.has_D ? ldf(vbase(p.D, h, 0), p.D.dtype, 0) : 0.0f;
+  const auto rq = make_buf(p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1], (uint32_t)P * N);
+  const auto rm = make_buf(p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1], (uint32_t)P * (N / 2));
+  const auto re = make_buf(p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1], (uint32_t)P * (N / 16));
+  const auto rx = make_buf(vbase(p.x, b, h), p.x_span);
+  const auto rz = make_buf(vbase(p.z, b, h), p.z_span);  // span 0 without z: loads return 0
   const int grp = h / p.ratio;
-  float Bd[16], Cv[16];
-  load16<true>(vbase(p.B, b, grp), LQ_BF16, 1, n0, Bd);
-  load16<true>(vbase(p.C, b, grp), LQ_BF16, 1, n0, Cv);
+  const auto rB = make_buf(vbase(p.B, b, grp), N * 2);
+  const auto rC = make_buf(vbase(p.C, b, grp), N * 2);
+
+  int pp[R];
+  u32x4_t qw[R];
+  u32x2_t mw[R];
+  uint32_t ev[R], xw[R], zw[R], xsh[R], zsh[R];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) Bd[i] *= dtv;
+  for (int r = 0; r < R; ++r) {
+    pp[r] = blockIdx.x * (R * SLOTS) + r * SLOTS + slot;
+    const uint32_t pc = (uint32_t)min(pp[r], P - 1);
+    const uint32_t qo = pc * N + n0;
+    qw[r] = __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 0, 0);
+    mw[r] = __builtin_amdgcn_raw_buffer_load_b64(rm, qo >> 1, 0, 0);
+    ev[r] = __builtin_amdgcn_raw_buffer_load_b8(re, qo >> 4, 0, 0);
+    const uint32_t xo = pc * p.x_row_bytes;
+    xw[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, xo & ~3u, 0, 0);
+    xsh[r] = (xo & 2u) * 8u;
+    const uint32_t zo = pc * p.z_row_bytes;
+    zw[r] = __builtin_amdgcn_raw_buffer_load_b32(rz, zo & ~3u, 0, 0);
+    zsh[r] = (zo & 2u) * 8u;
+  }
+  const u32x4_t bw0 = __builtin_amdgcn_raw_buffer_load_b128(rB, n0 * 2, 0, 0);
+  const u32x4_t bw1 = __builtin_amdgcn_raw_buffer_load_b128(rB, n0 * 2 + 16, 0, 0);
+  const u32x4_t cw0 = __builtin_amdgcn_raw_buffer_load_b128(rC, n0 * 2, 0, 0);
+  const u32x4_t cw1 = __builtin_amdgcn_raw_buffer_load_b128(rC, n0 * 2 + 16, 0, 0);
+
+  // head scalars (ms.py:134-139): without dt_bias or D the host points their views at dt with
+  // zero strides, so every scalar load is unconditional. exp and log use the hardware
+  // transcendentals (relative error ~1e-6, far inside the 2e-3 output tolerance)
+  float dtv = uniform_elem(vbase(p.dt, b, h), p.dt.dtype);
+  const float dtb = uniform_elem(vbase(p.dtb, h, 0), p.dtb.dtype);
+  const float av = uniform_elem(vbase(p.A, h, 0), p.A.dtype);
+  const float dv = uniform_elem(vbase(p.D, h, 0), p.D.dtype);
+  if (p.has_dtb) dtv += dtb;
+  if (p.softplus) dtv = dtv <= 20.0f ? __logf(1.0f + __expf(dtv)) : dtv;
+  const float dA = __expf(av * dtv);
+
+  float Bd[16], Cv[16];
+  {
+    const uint32_t bw[8] = {bw0.x, bw0.y, bw0.z, bw0.w, bw1.x, bw1.y, bw1.z, bw1.w};
+    const uint32_t cw[8] = {cw0.x, cw0.y, cw0.z, cw0.w, cw1.x, cw1.y, cw1.z, cw1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      Bd[2 * i] = __uint_as_float(bw[i] << 16) * dtv;
+      Bd[2 * i + 1] = __uint_as_float(bw[i] & 0xffff0000u) * dtv;
+      Cv[2 * i] = __uint_as_float(cw[i] << 16);
+      Cv[2 * i + 1] = __uint_as_float(cw[i] & 0xffff0000u);
+    }
+  }
+  const auto ro = make_buf(vbase(p.out, b, h), p.out_span);
 
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    // h' = h * exp(A dt) + (B dt) x, with the decay folded into the pair scale (exact)
+    const bool act = pp[r] < P;
+    const float xv = word_elem(xw[r], xsh[r], p.x.dtype);
+    // h' = h * exp(A dt) + (B dt) x, with the decay folded into the two pair scales (exact)
+    const float s0 = __uint_as_float(ev[r] << 23) * dA;
+    const float s1 = __uint_as_float((ev[r] + 1u) << 23) * dA;
+    const uint32_t qa[4] = {qw[r].x, qw[r].y, qw[r].z, qw[r].w};
+    const uint32_t ma[2] = {mw[r].x, mw[r].y};
     float hv[16];
-    const uint32_t evs = ev[r] << 23;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const uint32_t mi = (mw[r][k >> 2] >> (8 * (k & 3))) & 0xffu;
-      const float sdA = __uint_as_float((mi << 23) + evs) * dA;
+      const float sk = ((ma[k >> 2] >> (8 * (k & 3))) & 0xffu) ? s1 : s0;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int n = 2 * k + i;
-        const float qv = (float)(int)(int8_t)(qw[r][n >> 2] >> (8 * (n & 3)));
-        hv[n] = fmaf(qv, sdA, Bd[n] * xv[r]);
+        const float qv = (float)(int)(int8_t)(qa[n >> 2] >> (8 * (n & 3)));
+        hv[n] = fmaf(qv, sk, Bd[n] * xv);
       }
     }
     float ypart = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) ypart = fmaf(hv[i], Cv[i], ypart);
-    const float y0 = row_sum<BPR_LOG2>(ypart);
-    if (act[r] && blk == 0) {
-      float y = y0;
-      if (p.has_D) y += xv[r] * Dh;
-      if (p.has_z) y *= ldf(vbase(p.z, b, h), p.z.dtype, __umul24(pp[r], (uint32_t)p.z.s[2]));
-      char* ob = (char*)vbase(p.out, b, h);
-      const int oi = __umul24(pp[r], (uint32_t)p.out.s[2]);
-      if (p.out.dtype == LQ_BF16) {
-        ((uint16_t*)ob)[oi] = float_to_bf16_bits(y);
-      } else if (p.out.dtype == LQ_F16) {
-        ((_Float16*)ob)[oi] = (_Float16)y;
+    float y = row_sum<BPR_LOG2>(ypart);
+    if (p.has_D) y += xv * dv;
+    if (p.has_z) y *= word_elem(zw[r], zsh[r], p.z.dtype);
+    if (act && blk == 0) {
+      const uint32_t oo = (uint32_t)pp[r] * p.out_row_bytes;
+      if (p.out.dtype == LQ_F32) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), ro, oo, 0, 0);
+      } else if (p.out.dtype == LQ_BF16) {
+        __builtin_amdgcn_raw_buffer_store_b16(float_to_bf16_bits(y), ro, oo, 0, 0);
       } else {
-        ((float*)ob)[oi] = y;
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)y), ro, oo, 0, 0);
       }
     }
 
     // writeback encode (ms.py:168-222, 512-544)
     uint32_t qo[4], mo[2], eo;
     if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
-      const uint32_t idx = ((uint32_t)((b * p.H + h) * p.P + pp[r]) * (uint32_t)N + (uint32_t)n0) >> 1;
+      const uint32_t idx = ((uint32_t)((b * p.H + h) * P + pp[r]) * N + n0) >> 1;
       uint32_t base = (p.lo_base + idx) ^ p.kh;
       base ^= base >> 16;
       uint32_t pw[8];
@@ -614,10 +710,15 @@ __global__ __launch_bounds__(256) void mx_update_rows_kernel(MxUpdateParams p) {
       encode16_dither<FB>(hv, pw, qo, mo, eo);
     } else {
       float u16[16];
-      block_u16<RMODE>(p.uni, b, h, act[r] ? pp[r] : p.P - 1, n0, u16);
+      block_u16<RMODE>(p.uni, b, h, act ? pp[r] : P - 1, (int)n0, u16);
       encode16<FB, RMODE>(hv, u16, qo, mo, eo);
     }
-    if (act[r]) store_block<true>(qb + pp[r] * N, mb + pp[r] * (N / 2), eb + pp[r] * (N / 16), qo, mo, eo);
+    if (act) {
+      const uint32_t so = (uint32_t)pp[r] * N + n0;
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{qo[0], qo[1], qo[2], qo[3]}, rq, so, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{mo[0], mo[1]}, rm, so >> 1, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)eo, re, so >> 4, 0, 0);
+    }
   }
 }
 
@@ -846,24 +947,36 @@ static void dispatch_encode(const MxCodecParams& p, int rmode, bool vec, dim3 gr
   }
 }
 
+// Rows kernel geometry: R rows per lane, THREADS threads, one (batch, head) slice of up to
+// R * THREADS / (N/16) rows per workgroup (64 rows = one Nemotron-H head at N = 128).
+#ifndef LQ_MX_ROWS_R
+#define LQ_MX_ROWS_R 2
+#endif
+#ifndef LQ_MX_ROWS_THREADS
+#define LQ_MX_ROWS_THREADS 256
+#endif
+constexpr int ROWS_R = LQ_MX_ROWS_R;
+constexpr int ROWS_THREADS = LQ_MX_ROWS_THREADS;
+
 template <int FB, int BPR_LOG2>
 static void launch_rows(const MxUpdateParams& p, int rmode, dim3 grid, hipStream_t st) {
-  const dim3 block(256);
+  constexpr int R = ROWS_R, T = ROWS_THREADS;
+  const dim3 block(T);
   switch (rmode) {
     case LQ_ROUND_NEAREST_EVEN:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_NEAREST_EVEN, BPR_LOG2>), grid,
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_NEAREST_EVEN, BPR_LOG2, R, T>), grid,
                          block, 0, st, p);
       break;
     case LQ_ROUND_HALF_UP:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_HALF_UP, BPR_LOG2>), grid, block, 0,
-                         st, p);
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_HALF_UP, BPR_LOG2, R, T>), grid,
+                         block, 0, st, p);
       break;
     case LQ_ROUND_SR_UNIFORM:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_UNIFORM, BPR_LOG2>), grid,
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_UNIFORM, BPR_LOG2, R, T>), grid,
                          block, 0, st, p);
       break;
     default:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_COUNTER, BPR_LOG2>), grid,
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_COUNTER, BPR_LOG2, R, T>), grid,
                          block, 0, st, p);
       break;
   }
@@ -891,9 +1004,10 @@ static bool rows_path_ok(const MxUpdateParams& p, bool vec, bool bcvec, const lq
   if (p.N != 64 && p.N != 128 && p.N != 256) return false;
   if (p.st.qs[2] != p.N || p.st.ms[2] != p.N / 2 || p.st.es[2] != p.N / 16) return false;
   if (dt->stride[2] != 0 || A->stride[1] != 0 || A->stride[2] != 0) return false;
-  // per-row offsets of x, z and out are 24-bit products
-  const int64_t lim = (int64_t)1 << 23;
+  // byte offsets of x, z and out rows within a (batch, head) slice are 32-bit
+  const int64_t lim = (int64_t)1 << 28;
   if (p.P * p.x.s[2] >= lim || p.P * p.out.s[2] >= lim || p.P * p.z.s[2] >= lim) return false;
+  if (p.x.s[2] < 0 || p.out.s[2] < 0 || p.z.s[2] < 0) return false;
   if (dt_bias != nullptr && dt_bias->stride[1] != 0) return false;
   if (D != nullptr && D->stride[1] != 0) return false;
   if (round_mode == LQ_ROUND_SR_COUNTER) {
@@ -1008,7 +1122,28 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
   if (rows_path_ok(p, vec, bcvec, dt, dt_bias, A, D, round_mode, Bn * H * P * N)) {
     p.lo_base = (uint32_t)(rng_offset >> 1);
     p.kh = lowbias32_host((uint32_t)(rng_offset >> 33) ^ p.key);
-    const int rows = ROWS_PER_LANE * (256 >> p.vbpr_log2);
+    // per-row byte strides and slice spans of x, z and out
+    auto row_bytes = [](const View& v) { return (uint32_t)(v.s[2] * dtype_size(v.dtype)); };
+    auto span = [&](const View& v) {
+      return (uint32_t)((((P - 1) * v.s[2] + 1) * dtype_size(v.dtype) + 3) & ~(int64_t)3);
+    };
+    p.x_row_bytes = row_bytes(p.x);
+    p.x_span = span(p.x);
+    p.out_row_bytes = row_bytes(p.out);
+    p.out_span = span(p.out);
+    if (p.has_z) {
+      p.z_row_bytes = row_bytes(p.z);
+      p.z_span = span(p.z);
+    } else {  // a zero-span descriptor on x: its loads return 0 without reading memory
+      p.z = p.x;
+      p.z_row_bytes = 0;
+      p.z_span = 0;
+    }
+    // absent dt_bias or D: read dt's first element instead (the value is not used)
+    const View dt0{p.dt.data, p.dt.dtype, {0, 0, 0, 0}};
+    if (!p.has_dtb) p.dtb = dt0;
+    if (!p.has_D) p.D = dt0;
+    const int rows = ROWS_R * (ROWS_THREADS >> p.vbpr_log2);
     const dim3 rgrid((unsigned)((P + rows - 1) / rows), (unsigned)H, (unsigned)Bn);
     if (format_bits == 8) {
       dispatch_rows<8>(p, round_mode, rgrid, s);
