@@ -287,6 +287,8 @@ def main():
     kernels = {}
     for name, nbytes in sizes.items():
         us = ev.mean_us(name)
+        if us is None:  # no such layer in this configuration
+            continue
         gbs = nbytes / (us * 1e-6) / 1e9
         kernels[name] = {"us": round(us, 2), "algorithmic_bytes": nbytes,
                          "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),

@@ -224,6 +224,28 @@ __device__ __forceinline__ float max_with_zero(float a, float b) {
   return r;
 }
 
+// t + (w & 0xffff) and t + (w >> 16) as single SDWA adds.
+__device__ __forceinline__ int add_word0(int t, uint32_t w) {
+  int r;
+  asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
+      : "=v"(r) : "v"(t), "v"(w));
+  return r;
+}
+__device__ __forceinline__ int add_word1(int t, uint32_t w) {
+  int r;
+  asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+      : "=v"(r) : "v"(t), "v"(w));
+  return r;
+}
+
+// Keeps a value opaque to the optimiser, so that two precomputed alternatives stay two registers
+// and a select between them is not rewritten into a select of their inputs.
+template <typename T>
+__device__ __forceinline__ T pin(T v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 // Pair maxima and the block absmax of 16 values, max(0, |v_0|, ..., |v_15|) with NaNs ignored
 // (IEEE maxNum), as a running fmaxf from 0 gives.
 __device__ __forceinline__ float pair_maxima(const float (&v)[16], float (&pa)[8]) {
@@ -305,8 +327,8 @@ __device__ __forceinline__ void encode16_dither(const float (&v)[16], const uint
   int eb, ebase;
   const bool band = block_exponent_fast<FB>(amax, eb, ebase);
   const float thr = M * __uint_as_float((uint32_t)ebase << 23);
-  const int sh0 = 143 - ebase;
-  const int sh1 = sh0 - 1;
+  const int sh0 = pin(143 - ebase);
+  const int sh1 = pin(142 - ebase);
   float t[16];
   uint32_t mb[8];
 #pragma unroll
@@ -324,8 +346,8 @@ __device__ __forceinline__ void encode16_dither(const float (&v)[16], const uint
   int sum[16];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    sum[2 * k] = (int)t[2 * k] + (int)(pw[k] & 0xffffu);
-    sum[2 * k + 1] = (int)t[2 * k + 1] + (int)(pw[k] >> 16);
+    sum[2 * k] = add_word0((int)t[2 * k], pw[k]);
+    sum[2 * k + 1] = add_word1((int)t[2 * k + 1], pw[k]);
   }
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
@@ -553,6 +575,13 @@ __device__ __forceinline__ float row_sum(float v) {
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+// Cache policy bits of the state's buffer loads and stores (gfx950 CPol: sc0 = 1, nt = 2,
+// sc1 = 16). Every state byte is read once and written once per call, and one call's 212 MB
+// (batch 64) would only evict other data from L2 and the Infinity Cache: loads stream (nt),
+// stores stream through to memory (nt | sc1). Measured at batch 64, MX4: 51 us with default
+// policy, 48.6 us with nt loads only, 44.3-45.4 us with streaming stores as well.
+constexpr int STATE_LOAD_POLICY = 2;
+constexpr int STATE_STORE_POLICY = 18;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, BUF_DWORD3);
@@ -578,92 +607,119 @@ __device__ __forceinline__ float uniform_elem(const char* addr, int dtype) {
 // Update of the model's decode call (ms.py:97-222, 289-544 for the Nemotron-H layout): state rows
 // contiguous (row stride N), B and C bf16 with a contiguous d_state, and dt, dt_bias, A and D
 // constant within a head (stride 0 along head_dim, A also along d_state), as the model passes
-// them. Grid (ceil(P / (R * SLOTS)), H, B), THREADS threads; lane (slot, blk) owns block column
-// blk of rows slot + r * SLOTS (r < R, SLOTS = THREADS / (N/16)), so B*dt and C are decoded once
-// for R rows, and every wave load covers consecutive state rows.
-// Every load of a lane (R state blocks, R x values, B, C, the head scalars) is issued before the
-// first use of any of them; all lane offsets are 32-bit offsets into per-(batch, head) buffer
-// descriptors. Same arithmetic as mx_update_kernel in the (B*dt)*x order; in the counter mode
-// rng_offset is a multiple of 16, so a block's pair counters are lo0 | k and lowbias32's first
-// step folds into one per-block word.
-template <int FB, int RMODE, int BPR_LOG2, int R, int THREADS>
-__global__ __launch_bounds__(THREADS) void mx_update_rows_kernel(MxUpdateParams p) {
-  constexpr int BPR = 1 << BPR_LOG2;
-  constexpr uint32_t N = 16 * BPR;
-  constexpr int SLOTS = THREADS >> BPR_LOG2;
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int blk = threadIdx.x & (BPR - 1);
-  const int slot = threadIdx.x >> BPR_LOG2;
-  const uint32_t n0 = (uint32_t)blk * 16u;
-  const int P = p.P;
+// them. A workgroup of THREADS lanes covers up to R * SLOTS rows of one (batch, head) slice
+// (SLOTS = THREADS / (N/16)); lane (slot, blk) owns block column blk of rows slot + r * SLOTS,
+// r < R, so B*dt and C are decoded once for R rows and every wave load covers consecutive rows.
+// Lane offsets are 32-bit offsets into per-(batch, head) buffer descriptors. Same arithmetic as
+// mx_update_kernel in the (B*dt)*x order; in the counter mode rng_offset is a multiple of 16, so a
+// block's pair counters are lo0 | k and lowbias32's first step folds into one per-block word.
+#ifndef LQ_MX_ROWS_WAVES
+#define LQ_MX_ROWS_WAVES 1
+#endif
 
-  const auto rq = make_buf(p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1], (uint32_t)P * N);
-  const auto rm = make_buf(p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1], (uint32_t)P * (N / 2));
-  const auto re = make_buf(p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1], (uint32_t)P * (N / 16));
-  const auto rx = make_buf(vbase(p.x, b, h), p.x_span);
-  const auto rz = make_buf(vbase(p.z, b, h), p.z_span);  // span 0 without z: loads return 0
-  const int grp = h / p.ratio;
-  const auto rB = make_buf(vbase(p.B, b, grp), N * 2);
-  const auto rC = make_buf(vbase(p.C, b, grp), N * 2);
+// State blocks and x words of R rows of one lane (the raw loads of one work item).
+template <int R>
+struct RowLoads {
+  u32x4_t q[R];
+  u32x2_t m[R];
+  uint32_t e[R], xw[R], zw[R];
+};
 
-  int pp[R];
-  u32x4_t qw[R];
-  u32x2_t mw[R];
-  uint32_t ev[R], xw[R], zw[R], xsh[R], zsh[R];
+// Buffer descriptors of one (batch, head) slice.
+struct HeadBufs {
+  __amdgpu_buffer_rsrc_t q, m, e, x, z, out;
+};
+
+template <uint32_t N>
+__device__ __forceinline__ HeadBufs head_bufs(const MxUpdateParams& p, int b, int h) {
+  HeadBufs hb;
+  const uint32_t P = (uint32_t)p.P;
+  hb.q = make_buf(p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1], P * N);
+  hb.m = make_buf(p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1], P * (N / 2));
+  hb.e = make_buf(p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1], P * (N / 16));
+  hb.x = make_buf(vbase(p.x, b, h), p.x_span);
+  hb.z = make_buf(vbase(p.z, b, h), p.z_span);  // span 0 without z: its loads return 0
+  hb.out = make_buf(vbase(p.out, b, h), p.out_span);
+  return hb;
+}
+
+// Issues the loads of rows row0 + r * SLOTS + slot (clamped to P - 1) of one slice.
+template <int R, int SLOTS, uint32_t N>
+__device__ __forceinline__ void load_rows(const MxUpdateParams& p, const HeadBufs& hb, int row0,
+                                          int slot, uint32_t n0, RowLoads<R>& L) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    pp[r] = blockIdx.x * (R * SLOTS) + r * SLOTS + slot;
-    const uint32_t pc = (uint32_t)min(pp[r], P - 1);
+    const uint32_t pc = (uint32_t)min(row0 + r * SLOTS + slot, p.P - 1);
     const uint32_t qo = pc * N + n0;
-    qw[r] = __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 0, 0);
-    mw[r] = __builtin_amdgcn_raw_buffer_load_b64(rm, qo >> 1, 0, 0);
-    ev[r] = __builtin_amdgcn_raw_buffer_load_b8(re, qo >> 4, 0, 0);
-    const uint32_t xo = pc * p.x_row_bytes;
-    xw[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, xo & ~3u, 0, 0);
-    xsh[r] = (xo & 2u) * 8u;
-    const uint32_t zo = pc * p.z_row_bytes;
-    zw[r] = __builtin_amdgcn_raw_buffer_load_b32(rz, zo & ~3u, 0, 0);
-    zsh[r] = (zo & 2u) * 8u;
+    L.q[r] = __builtin_amdgcn_raw_buffer_load_b128(hb.q, qo, 0, STATE_LOAD_POLICY);
+    L.m[r] = __builtin_amdgcn_raw_buffer_load_b64(hb.m, qo >> 1, 0, STATE_LOAD_POLICY);
+    L.e[r] = __builtin_amdgcn_raw_buffer_load_b8(hb.e, qo >> 4, 0, STATE_LOAD_POLICY);
+    L.xw[r] = __builtin_amdgcn_raw_buffer_load_b32(hb.x, (pc * p.x_row_bytes) & ~3u, 0, 0);
+    L.zw[r] = __builtin_amdgcn_raw_buffer_load_b32(hb.z, (pc * p.z_row_bytes) & ~3u, 0, 0);
   }
-  const u32x4_t bw0 = __builtin_amdgcn_raw_buffer_load_b128(rB, n0 * 2, 0, 0);
-  const u32x4_t bw1 = __builtin_amdgcn_raw_buffer_load_b128(rB, n0 * 2 + 16, 0, 0);
-  const u32x4_t cw0 = __builtin_amdgcn_raw_buffer_load_b128(rC, n0 * 2, 0, 0);
-  const u32x4_t cw1 = __builtin_amdgcn_raw_buffer_load_b128(rC, n0 * 2 + 16, 0, 0);
+}
 
-  // head scalars (ms.py:134-139): without dt_bias or D the host points their views at dt with
-  // zero strides, so every scalar load is unconditional. exp and log use the hardware
-  // transcendentals (relative error ~1e-6, far inside the 2e-3 output tolerance)
+// 16 bf16 values of B or C for the lane's block column (two 16-byte loads).
+__device__ __forceinline__ void load_bc(const MxUpdateParams& p, int b, int grp, uint32_t n0,
+                                        uint32_t N, u32x4_t (&bw)[2], u32x4_t (&cw)[2]) {
+  const auto rB = make_buf(vbase(p.B, b, grp), N * 2);
+  const auto rC = make_buf(vbase(p.C, b, grp), N * 2);
+  bw[0] = __builtin_amdgcn_raw_buffer_load_b128(rB, n0 * 2, 0, 0);
+  bw[1] = __builtin_amdgcn_raw_buffer_load_b128(rB, n0 * 2 + 16, 0, 0);
+  cw[0] = __builtin_amdgcn_raw_buffer_load_b128(rC, n0 * 2, 0, 0);
+  cw[1] = __builtin_amdgcn_raw_buffer_load_b128(rC, n0 * 2 + 16, 0, 0);
+}
+
+__device__ __forceinline__ void expand_bf16(const u32x4_t (&w)[2], float (&o)[16]) {
+  const uint32_t a[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    o[2 * i] = __uint_as_float(a[i] << 16);
+    o[2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+  }
+}
+
+// Head scalars (ms.py:134-139): dt (+ dt_bias, softplus), exp(A dt) and D of head h. Without
+// dt_bias or D the host points their views at dt with zero strides, so every scalar load is
+// unconditional. exp and log use the hardware transcendentals (relative error ~1e-6, far inside
+// the 2e-3 output tolerance).
+struct HeadScalars {
+  float dt, dA, D;
+};
+
+__device__ __forceinline__ HeadScalars head_scalars(const MxUpdateParams& p, int b, int h) {
+  HeadScalars s;
   float dtv = uniform_elem(vbase(p.dt, b, h), p.dt.dtype);
   const float dtb = uniform_elem(vbase(p.dtb, h, 0), p.dtb.dtype);
   const float av = uniform_elem(vbase(p.A, h, 0), p.A.dtype);
-  const float dv = uniform_elem(vbase(p.D, h, 0), p.D.dtype);
+  s.D = uniform_elem(vbase(p.D, h, 0), p.D.dtype);
   if (p.has_dtb) dtv += dtb;
   if (p.softplus) dtv = dtv <= 20.0f ? __logf(1.0f + __expf(dtv)) : dtv;
-  const float dA = __expf(av * dtv);
+  s.dt = dtv;
+  s.dA = __expf(av * dtv);
+  return s;
+}
 
-  float Bd[16], Cv[16];
-  {
-    const uint32_t bw[8] = {bw0.x, bw0.y, bw0.z, bw0.w, bw1.x, bw1.y, bw1.z, bw1.w};
-    const uint32_t cw[8] = {cw0.x, cw0.y, cw0.z, cw0.w, cw1.x, cw1.y, cw1.z, cw1.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      Bd[2 * i] = __uint_as_float(bw[i] << 16) * dtv;
-      Bd[2 * i + 1] = __uint_as_float(bw[i] & 0xffff0000u) * dtv;
-      Cv[2 * i] = __uint_as_float(cw[i] << 16);
-      Cv[2 * i + 1] = __uint_as_float(cw[i] & 0xffff0000u);
-    }
-  }
-  const auto ro = make_buf(vbase(p.out, b, h), p.out_span);
-
+// Update, y, and writeback encode of the R rows held in L.
+template <int FB, int RMODE, int BPR_LOG2, int R, int SLOTS>
+__device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadBufs& hb, int b,
+                                            int h, int row0, int slot, int blk,
+                                            const RowLoads<R>& L, const float (&Bd)[16],
+                                            const float (&Cv)[16], const HeadScalars& hs) {
+  constexpr uint32_t N = 16u << BPR_LOG2;
+  const uint32_t n0 = (uint32_t)blk * 16u;
+  const int P = p.P;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const bool act = pp[r] < P;
-    const float xv = word_elem(xw[r], xsh[r], p.x.dtype);
+    const int pp = row0 + r * SLOTS + slot;
+    const bool act = pp < P;
+    const uint32_t pc = (uint32_t)min(pp, P - 1);
+    const float xv = word_elem(L.xw[r], ((pc * p.x_row_bytes) & 2u) * 8u, p.x.dtype);
     // h' = h * exp(A dt) + (B dt) x, with the decay folded into the two pair scales (exact)
-    const float s0 = __uint_as_float(ev[r] << 23) * dA;
-    const float s1 = __uint_as_float((ev[r] + 1u) << 23) * dA;
-    const uint32_t qa[4] = {qw[r].x, qw[r].y, qw[r].z, qw[r].w};
-    const uint32_t ma[2] = {mw[r].x, mw[r].y};
+    const float s0 = pin(__uint_as_float(L.e[r] << 23) * hs.dA);
+    const float s1 = pin(__uint_as_float((L.e[r] + 1u) << 23) * hs.dA);
+    const uint32_t qa[4] = {L.q[r].x, L.q[r].y, L.q[r].z, L.q[r].w};
+    const uint32_t ma[2] = {L.m[r].x, L.m[r].y};
     float hv[16];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -679,23 +735,24 @@ __global__ __launch_bounds__(THREADS) void mx_update_rows_kernel(MxUpdateParams 
 #pragma unroll
     for (int i = 0; i < 16; ++i) ypart = fmaf(hv[i], Cv[i], ypart);
     float y = row_sum<BPR_LOG2>(ypart);
-    if (p.has_D) y += xv * dv;
-    if (p.has_z) y *= word_elem(zw[r], zsh[r], p.z.dtype);
+    if (p.has_D) y += xv * hs.D;
+    if (p.has_z) y *= word_elem(L.zw[r], ((pc * p.z_row_bytes) & 2u) * 8u, p.z.dtype);
     if (act && blk == 0) {
-      const uint32_t oo = (uint32_t)pp[r] * p.out_row_bytes;
+      const uint32_t oo = (uint32_t)pp * p.out_row_bytes;
       if (p.out.dtype == LQ_F32) {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), ro, oo, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), hb.out, oo, 0, 0);
       } else if (p.out.dtype == LQ_BF16) {
-        __builtin_amdgcn_raw_buffer_store_b16(float_to_bf16_bits(y), ro, oo, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(float_to_bf16_bits(y), hb.out, oo, 0, 0);
       } else {
-        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)y), ro, oo, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)y), hb.out,
+                                              oo, 0, 0);
       }
     }
 
     // writeback encode (ms.py:168-222, 512-544)
     uint32_t qo[4], mo[2], eo;
     if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
-      const uint32_t idx = ((uint32_t)((b * p.H + h) * P + pp[r]) * N + n0) >> 1;
+      const uint32_t idx = ((uint32_t)((b * p.H + h) * P + pp) * N + n0) >> 1;
       uint32_t base = (p.lo_base + idx) ^ p.kh;
       base ^= base >> 16;
       uint32_t pw[8];
@@ -710,16 +767,46 @@ __global__ __launch_bounds__(THREADS) void mx_update_rows_kernel(MxUpdateParams 
       encode16_dither<FB>(hv, pw, qo, mo, eo);
     } else {
       float u16[16];
-      block_u16<RMODE>(p.uni, b, h, act ? pp[r] : P - 1, (int)n0, u16);
+      block_u16<RMODE>(p.uni, b, h, (int)pc, (int)n0, u16);
       encode16<FB, RMODE>(hv, u16, qo, mo, eo);
     }
     if (act) {
-      const uint32_t so = (uint32_t)pp[r] * N + n0;
-      __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{qo[0], qo[1], qo[2], qo[3]}, rq, so, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{mo[0], mo[1]}, rm, so >> 1, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)eo, re, so >> 4, 0, 0);
+      const uint32_t so = (uint32_t)pp * N + n0;
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{qo[0], qo[1], qo[2], qo[3]}, hb.q, so, 0,
+                                             STATE_STORE_POLICY);
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{mo[0], mo[1]}, hb.m, so >> 1, 0,
+                                            STATE_STORE_POLICY);
+      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)eo, hb.e, so >> 4, 0, STATE_STORE_POLICY);
     }
   }
+}
+
+// One work item per workgroup: grid (ceil(P / (R * SLOTS)), H, B). Every load of the lane (R state
+// blocks, x, B, C, the head scalars) is issued before the first use of any of them.
+template <int FB, int RMODE, int BPR_LOG2, int R, int THREADS>
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(LQ_MX_ROWS_WAVES)))
+void mx_update_rows_kernel(MxUpdateParams p) {
+  constexpr int BPR = 1 << BPR_LOG2;
+  constexpr uint32_t N = 16 * BPR;
+  constexpr int SLOTS = THREADS >> BPR_LOG2;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int blk = threadIdx.x & (BPR - 1);
+  const int slot = threadIdx.x >> BPR_LOG2;
+  const uint32_t n0 = (uint32_t)blk * 16u;
+  const int row0 = blockIdx.x * (R * SLOTS);
+
+  const HeadBufs hb = head_bufs<N>(p, b, h);
+  RowLoads<R> L;
+  load_rows<R, SLOTS, N>(p, hb, row0, slot, n0, L);
+  u32x4_t bw[2], cw[2];
+  load_bc(p, b, h / p.ratio, n0, N, bw, cw);
+  const HeadScalars hs = head_scalars(p, b, h);
+  float Bd[16], Cv[16];
+  expand_bf16(bw, Bd);
+  expand_bf16(cw, Cv);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) Bd[i] *= hs.dt;
+  update_rows<FB, RMODE, BPR_LOG2, R, SLOTS>(p, hb, b, h, row0, slot, blk, L, Bd, Cv, hs);
 }
 
 template <int FB, int RMODE, bool VEC>
