@@ -156,6 +156,23 @@ int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* shared_exp,
                        const lq_tensor* out, int format_bits, int dt_softplus, int round_mode,
                        const lq_tensor* uniform, uint64_t seed, uint64_t rng_offset, void* stream);
 
+/*
+ * Selective-state update of an unquantized (bf16, fp16 or fp32) Mamba2 state, in place:
+ *   dt = dt (+ dt_bias); dt = softplus(dt) if dt_softplus (x <= 20 ? log(1+e^x) : x)
+ *   h' = h * exp(A * dt) + (B * dt) * x  (fp32, one fma per element, stored back with RNE)
+ *   y  = sum_n h' * C (+ x * D);  y *= z * sigmoid(z) when z is given
+ * Replaces mamba-ssm 2.3.2.post1's selective_state_update, which the reference calls for every
+ * layer whose state is not registered for the MX kernel (the `original` fallback of
+ * hybrid_quant/mamba_state_8b_kernel.py:738-747) and which is the bf16-state baseline of its
+ * state experiments. Shapes as lq_mx_state_update with state [B,H,P,N] in place of the MX
+ * tensors; every tensor may have any strides (0 allowed), the state a 16-byte aligned contiguous
+ * last dimension for vector access.
+ */
+int lq_selective_state_update(const lq_tensor* state, const lq_tensor* x, const lq_tensor* dt,
+                              const lq_tensor* dt_bias, const lq_tensor* A, const lq_tensor* B,
+                              const lq_tensor* C, const lq_tensor* D, const lq_tensor* z,
+                              const lq_tensor* out, int dt_softplus, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "lq_mx_encode",
     "lq_mx_decode",
     "lq_mx_state_update",
+    "lq_selective_state_update",
 )
 
 
@@ -95,6 +96,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.lq_mx_state_update.argtypes = [_P] * 12 + [
         ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_uint64, ctypes.c_uint64,
         ctypes.c_void_p]
+    lib.lq_selective_state_update.restype = ctypes.c_int
+    lib.lq_selective_state_update.argtypes = [_P] * 10 + [ctypes.c_int, ctypes.c_void_p]
 
 
 def lib() -> ctypes.CDLL:
@@ -255,4 +258,14 @@ def mx_state_update(q_state, shared_exp, micro_exp, x, dt, dt_bias, A, B, C, D, 
         1 if dt_softplus else 0, int(round_mode), desc(uniform), int(seed) & ((1 << 64) - 1),
         int(rng_offset), _stream(dev))
     check(rc, "lq_mx_state_update")
+    return out
+
+
+def selective_state_update(state, x, dt, dt_bias, A, B, C, D, z, out,
+                           dt_softplus: bool) -> torch.Tensor:
+    dev = _require_gpu(state, x, dt, dt_bias, A, B, C, D, z, out)
+    rc = lib().lq_selective_state_update(
+        desc(state), desc(x), desc(dt), desc(dt_bias), desc(A), desc(B), desc(C), desc(D),
+        desc(z), desc(out), 1 if dt_softplus else 0, _stream(dev))
+    check(rc, "lq_selective_state_update")
     return out

@@ -27,6 +27,7 @@
 #include <stdlib.h>
 
 #include "lq_common.h"
+#include "state_common.h"
 
 namespace lq {
 
@@ -61,50 +62,6 @@ struct MxCodecParams {
   uint32_t key;
   uint64_t rng_offset;
 };
-
-// Grid (ceil(P * vbpr / 256), H, B): one lane per 16-value block of one (b, h) pair; the N/16
-// block lanes of a state row are adjacent (vbpr = N/16 rounded up to a power of two). Batch and
-// head come from the block index, so every per-(b, h) offset is uniform and lane offsets are
-// 32-bit.
-struct LaneIdx {
-  int b, h, pp, blk;
-  bool in_range, active;
-};
-
-__device__ __forceinline__ LaneIdx lane_index(int P, int vbpr_log2, int bpr) {
-  LaneIdx L;
-  L.h = blockIdx.y;
-  L.b = blockIdx.z;
-  const int lanes = P << vbpr_log2;
-  int idx = blockIdx.x * 256 + threadIdx.x;
-  L.in_range = idx < lanes;
-  if (!L.in_range) idx = lanes - 1;  // whole trailing row groups only; they store nothing
-  L.pp = idx >> vbpr_log2;
-  const int blk = idx & ((1 << vbpr_log2) - 1);
-  L.active = L.in_range && blk < bpr;
-  L.blk = min(blk, bpr - 1);
-  return L;
-}
-
-__device__ __forceinline__ int dtype_bytes(int dtype) {
-  return dtype == LQ_F32 ? 4 : 2;
-}
-
-// uniform base of a strided float view at (i0, i1) of its leading dimensions
-__device__ __forceinline__ const char* vbase(const View& v, int i0, int i1) {
-  return (const char*)v.data + ((int64_t)i0 * v.s[0] + (int64_t)i1 * v.s[1]) * dtype_bytes(v.dtype);
-}
-
-__device__ __forceinline__ float ldf(const char* base, int dtype, int idx) {
-  switch (dtype) {
-    case LQ_BF16:
-      return bf16_bits_to_float(((const uint16_t*)base)[idx]);
-    case LQ_F16:
-      return (float)(((const _Float16*)base)[idx]);
-    default:
-      return ((const float*)base)[idx];
-  }
-}
 
 __device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
   x ^= x >> 16;
@@ -421,27 +378,6 @@ __device__ __forceinline__ void decode16(const uint32_t (&qw)[4], const uint32_t
   }
 }
 
-// 16 consecutive d_state values of B or C: vector loads for contiguous bf16 (BCVEC), else
-// strided element loads of any float dtype.
-template <bool BCVEC>
-__device__ __forceinline__ void load16(const char* base, int dtype, int stride, int n0,
-                                       float (&o)[16]) {
-  if constexpr (BCVEC) {
-    const uint4* p4 = (const uint4*)((const uint16_t*)base + n0);
-    const uint4 a = p4[0];
-    const uint4 b = p4[1];
-    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      o[2 * i] = __uint_as_float(w[i] << 16);
-      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] = ldf(base, dtype, (n0 + i) * stride);
-  }
-}
-
 // Supplied uniforms of one block (LQ_ROUND_SR_UNIFORM) scaled by 2^16; zeros otherwise.
 template <int RMODE>
 __device__ __forceinline__ void block_u16(const View& uni, int b, int h, int pp, int n0,
@@ -570,38 +506,6 @@ __device__ __forceinline__ float row_sum(float v) {
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
   }
   return v;
-}
-
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
-// Cache policy bits of the state's buffer loads and stores (gfx950 CPol: sc0 = 1, nt = 2,
-// sc1 = 16). Every state byte is read once and written once per call, and one call's 212 MB
-// (batch 64) would only evict other data from L2 and the Infinity Cache: loads stream (nt),
-// stores stream through to memory (nt | sc1). Measured at batch 64, MX4: 51 us with default
-// policy, 48.6 us with nt loads only, 44.3-45.4 us with streaming stores as well.
-constexpr int STATE_LOAD_POLICY = 2;
-constexpr int STATE_STORE_POLICY = 18;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, BUF_DWORD3);
-}
-
-// Float value of the 16- or 32-bit element held in the 32-bit word w at bit `shift` (0 or 16).
-__device__ __forceinline__ float word_elem(uint32_t w, uint32_t shift, int dtype) {
-  const uint32_t h16 = (w >> shift) & 0xffffu;
-  if (dtype == LQ_F32) return __uint_as_float(w);
-  if (dtype == LQ_BF16) return __uint_as_float(h16 << 16);
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
-}
-
-// Element at a wave-uniform address, read by a scalar load of the aligned 32-bit word holding it
-// (a 4-byte aligned word never crosses a page, so it stays inside the allocation's pages).
-__device__ __forceinline__ float uniform_elem(const char* addr, int dtype) {
-  typedef const __attribute__((address_space(4))) uint32_t* cword_t;
-  const uintptr_t a = (uintptr_t)addr;
-  const uint32_t w = *(cword_t)(a & ~(uintptr_t)3);
-  return word_elem(w, (uint32_t)(a & 2u) * 8u, dtype);
 }
 
 // Update of the model's decode call (ms.py:97-222, 289-544 for the Nemotron-H layout): state rows

@@ -9,6 +9,8 @@ torch initial encoder are replaced by HIP kernels for gfx950 behind the C ABI
     _state_update_mx8_kernel + _requantize_mx4_kernel -> lq_mx_state_update, format_bits 4
                                                      (ms.py:225-443, 494-544), one pass
     _quantize_initial_state_mx (torch)            -> lq_mx_encode, nearest-even (ms.py:547-572)
+    mamba-ssm selective_state_update (the fallback -> lq_selective_state_update (bf16/fp16/fp32
+    for unregistered layers, ms.py:738-747)           state), `selective_state_update` here
 
 Stochastic rounding. The reference draws Triton's tl.rand per element at offset
 step*B*H*P*N + element index. This module keeps those offsets and, by default, draws from the
@@ -178,6 +180,43 @@ def mx4_state_selective_update(*args, **kwargs) -> torch.Tensor:
     return mx_state_selective_update(*args, **kwargs)
 
 
+def selective_state_update(state: torch.Tensor, x: torch.Tensor, dt: torch.Tensor,
+                           A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
+                           D: torch.Tensor | None = None, z: torch.Tensor | None = None,
+                           dt_bias: torch.Tensor | None = None, dt_softplus: bool = False,
+                           state_batch_indices: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode step of an unquantized (bf16 / fp16 / fp32) Mamba2 state, in place, with
+    mamba-ssm 2.3.2.post1's selective_state_update interface: state [B,H,P,N] or [B,P,N];
+    x, dt, z [B,H,P] or [B,P]; A [H,P,N] or [P,N]; B, C [B,G,N] or [B,N]; D, dt_bias [H,P] or
+    [P]. fp32 arithmetic (h' = h*exp(A*dt) + (B*dt)*x, y = C.h' + D*x, y *= silu(z)); the state
+    is rounded back to its dtype. Returns y in x's dtype. This is the update the reference runs
+    for unregistered layers and as its bf16-state baseline (ms.py:738-747)."""
+    if state_batch_indices is not None:
+        raise NotImplementedError("state_batch_indices is not supported")
+    has_heads = state.dim() > 3
+    if state.dim() == 3:
+        state = state.unsqueeze(1)
+    if x.dim() == 2:
+        x = x.unsqueeze(1)
+    if dt.dim() == 2:
+        dt = dt.unsqueeze(1)
+    if A.dim() == 2:
+        A = A.unsqueeze(0)
+    if B.dim() == 2:
+        B = B.unsqueeze(1)
+    if C.dim() == 2:
+        C = C.unsqueeze(1)
+    if D is not None and D.dim() == 1:
+        D = D.unsqueeze(0)
+    if z is not None and z.dim() == 2:
+        z = z.unsqueeze(1)
+    if dt_bias is not None and dt_bias.dim() == 1:
+        dt_bias = dt_bias.unsqueeze(0)
+    out = torch.empty_like(x)
+    _abi.selective_state_update(state, x, dt, dt_bias, A, B, C, D, z, out, dt_softplus)
+    return out if has_heads else out.squeeze(1)
+
+
 def patch_nemotron_h_mamba_decode_state_kernel(model, group_size: int = MX8_BLOCK_SIZE,
                                                stochastic: bool = True, seed: int = 1234) -> None:
     """Rebind the remote module's selective_state_update (ms.py:732-767).
@@ -188,6 +227,8 @@ def patch_nemotron_h_mamba_decode_state_kernel(model, group_size: int = MX8_BLOC
     """
     module = __import__(model.__class__.__module__, fromlist=["selective_state_update"])
     original = getattr(module, "_mx_state_kernel_original", module.selective_state_update)
+    if original is None:  # the remote module found no mamba-ssm kernel: use the HIP update
+        original = selective_state_update
     module._mx_state_kernel_stochastic = stochastic
     module._mx_state_kernel_seed = seed
 

@@ -1,0 +1,197 @@
+"""GPU parity of the unquantized selective-state update (lq_selective_state_update, the
+mamba-ssm selective_state_update the reference falls back to and its bf16-state baseline)
+against the oracle's fp32 restatement: y within 2e-3; the stored state equal to the oracle's
+after rounding to the state dtype for >= 99.9% of elements and within one unit in the last place
+elsewhere (the kernel's fma rounds once where the oracle rounds twice); dt = 0 leaves the state
+bit-identical."""
+import pytest
+import torch
+
+from helpers import assert_close_rel
+from hybrid_quant import mamba_state_8b_kernel as ms
+from layer_quant_amd import _abi
+from oracle import mx_state as omx
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(bsz, nh, p_, n, ng, seed, head_const=True, z=False, dt_zero=False):
+    g = torch.Generator().manual_seed(seed)
+    if head_const:  # the model's layout: dt, A, D, dt_bias constant within a head
+        dt = torch.randn(bsz, nh, 1, generator=g).to(torch.bfloat16).expand(bsz, nh, p_)
+        A = (-torch.exp(torch.rand(nh, generator=g) * 2))[:, None, None].expand(nh, p_, n)
+        D = torch.randn(nh, generator=g)[:, None].expand(nh, p_)
+        dt_bias = (torch.randn(nh, generator=g) * 0.1)[:, None].expand(nh, p_)
+    else:
+        dt = torch.rand(bsz, nh, p_, generator=g)
+        A = -torch.rand(nh, p_, n, generator=g)
+        D = torch.randn(nh, p_, generator=g)
+        dt_bias = torch.randn(nh, p_, generator=g) * 0.1
+    if dt_zero:
+        dt = torch.zeros_like(dt)
+    return dict(
+        x=torch.randn(bsz, nh, p_, generator=g).to(torch.bfloat16),
+        dt=dt, A=A, D=D, dt_bias=dt_bias,
+        B=torch.randn(bsz, ng, n, generator=g).to(torch.bfloat16),
+        C=torch.randn(bsz, ng, n, generator=g).to(torch.bfloat16),
+        z=torch.randn(bsz, nh, p_, generator=g).to(torch.bfloat16) if z else None,
+    )
+
+
+def _to(t, dev):
+    return {k: (None if v is None else v.to(dev)) for k, v in t.items()}
+
+
+ULP = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10, torch.float32: 2.0 ** -23}
+
+
+def _assert_state_ulp(got: torch.Tensor, ref: torch.Tensor, frac=0.999):
+    """Bit-identical for >= frac of the elements; elsewhere within one ulp of the state dtype
+    (relative to |ref|) plus 1e-5 of the mean magnitude, which covers results that cancel to
+    nearly zero, where one fp32 rounding of the two terms moves many ulps of the result."""
+    assert got.dtype == ref.dtype
+    bits = {torch.bfloat16: torch.int16, torch.float16: torch.int16, torch.float32: torch.int32}
+    gi = got.cpu().contiguous().view(bits[got.dtype])
+    ri = ref.cpu().contiguous().view(bits[ref.dtype])
+    same = (gi == ri).double().mean().item()
+    assert same >= frac, f"only {same:.5f} of state values identical"
+    g = got.cpu().double()
+    r = ref.cpu().double()
+    bound = ULP[got.dtype] * r.abs() + 1e-5 * r.abs().mean()
+    worst = ((g - r).abs() / bound).max().item()
+    assert worst <= 1.0, f"state differs by {worst:.3g} x the one-ulp bound"
+
+
+@pytest.mark.parametrize("sdtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("n", [64, 128, 256])
+def test_update_model_layout(gpu, sdtype, n):
+    bsz, nh, p_, ng = 3, 16, 32, 4
+    g = torch.Generator().manual_seed(n)
+    h0 = (torch.randn(bsz, nh, p_, n, generator=g) * 0.5).to(sdtype)
+    t = _inputs(bsz, nh, p_, n, ng, 7 + n)
+    state = h0.to(gpu)
+    out = ms.selective_state_update(state, **{k: v for k, v in _to(t, gpu).items()},
+                                    dt_softplus=True)
+    ref_state, ref_y = omx.bf16_state_update(h0.float(), t["x"], t["dt"], t["A"], t["B"], t["C"],
+                                             t["D"], None, t["dt_bias"], True)
+    assert out.dtype == torch.bfloat16 and out.shape == (bsz, nh, p_)
+    assert_close_rel(out.float().cpu(), ref_y.to(torch.bfloat16).float(), rtol=8e-3, what="y")
+    ref_h = omx.update_math(h0.float(), t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], None,
+                            t["dt_bias"], True)[0]
+    if sdtype == torch.float32:
+        assert_close_rel(state.cpu(), ref_h, rtol=1e-5, what="fp32 state")
+    else:
+        _assert_state_ulp(state, ref_h.to(sdtype))
+    del ref_state
+
+
+def test_update_general_layout_z_f32_out(gpu):
+    """Per-element A, dt and D, a silu(z) gate, fp32 x and out, non-contiguous state rows."""
+    bsz, nh, p_, n, ng = 2, 8, 24, 128, 2
+    t = _inputs(bsz, nh, p_, n, ng, 3, head_const=False, z=True)
+    t["x"] = t["x"].float()
+    g = torch.Generator().manual_seed(4)
+    big = torch.randn(bsz, nh, p_ + 5, n, generator=g).to(torch.bfloat16)
+    h0 = big[:, :, :p_]  # row stride n, head stride (p_ + 5) * n
+    state = big.to(gpu)[:, :, :p_]
+    out = torch.empty(bsz, nh, p_, device=gpu)
+    d = _to(t, gpu)
+    _abi.selective_state_update(state, d["x"], d["dt"], d["dt_bias"], d["A"], d["B"], d["C"],
+                                d["D"], d["z"], out, False)
+    ref_h, ref_y = omx.bf16_state_update(h0.float(), t["x"], t["dt"], t["A"], t["B"], t["C"],
+                                         t["D"], t["z"], t["dt_bias"], False)
+    assert_close_rel(out.cpu(), ref_y, what="y")
+    _assert_state_ulp(state.contiguous(), ref_h)
+    assert torch.equal(big.to(gpu)[:, :, p_:].cpu(), big[:, :, p_:])
+
+
+def test_dt_zero_keeps_state(gpu):
+    bsz, nh, p_, n, ng = 2, 8, 64, 128, 8
+    g = torch.Generator().manual_seed(11)
+    h0 = (torch.randn(bsz, nh, p_, n, generator=g) * 0.5).to(torch.bfloat16)
+    t = _inputs(bsz, nh, p_, n, ng, 12, dt_zero=True)
+    t["dt_bias"] = None  # dt' = dt = 0: exp(A * 0) = 1 and (B * 0) * x = 0, so h' = h exactly
+    state = h0.to(gpu)
+    out = ms.selective_state_update(state, **_to(t, gpu), dt_softplus=False)
+    assert torch.equal(state.cpu(), h0)
+    ref_y = omx.update_math(h0.float(), t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], None,
+                            None, False)[1]
+    assert_close_rel(out.float().cpu(), ref_y.to(torch.bfloat16).float(), rtol=8e-3, what="y")
+
+
+def test_headless_forms_match(gpu):
+    """mamba-ssm's 3-D call forms (no head dimension) give the same result as the 4-D ones."""
+    bsz, p_, n = 4, 32, 64
+    g = torch.Generator().manual_seed(21)
+    h0 = (torch.randn(bsz, p_, n, generator=g) * 0.5).to(torch.bfloat16)
+    x = torch.randn(bsz, p_, generator=g).to(torch.bfloat16)
+    dt = torch.rand(bsz, p_, generator=g)
+    A = -torch.rand(p_, n, generator=g)
+    B = torch.randn(bsz, n, generator=g).to(torch.bfloat16)
+    C = torch.randn(bsz, n, generator=g).to(torch.bfloat16)
+    D = torch.randn(p_, generator=g)
+    s3 = h0.to(gpu)
+    y3 = ms.selective_state_update(s3, x.to(gpu), dt.to(gpu), A.to(gpu), B.to(gpu), C.to(gpu),
+                                   D=D.to(gpu), dt_softplus=True)
+    s4 = h0.unsqueeze(1).to(gpu)
+    y4 = ms.selective_state_update(s4, x[:, None].to(gpu), dt[:, None].to(gpu), A[None].to(gpu),
+                                   B[:, None].to(gpu), C[:, None].to(gpu), D=D[None].to(gpu),
+                                   dt_softplus=True)
+    assert y3.shape == (bsz, p_)
+    assert torch.equal(y3, y4[:, 0]) and torch.equal(s3, s4[:, 0])
+
+
+def test_full_size_b64_model_layout(gpu):
+    """Nemotron-H layer at batch 64 (128 heads x 64 x 128, 8 groups): three sampled batch rows
+    against the oracle's fp32 update, the state within one bf16 ulp of its rounding."""
+    bsz, nh, p_, n, ng = 64, 128, 64, 128, 8
+    g = torch.Generator(device=gpu).manual_seed(5)
+    state = (torch.randn(bsz, nh, p_, n, device=gpu, generator=g) * 0.5).to(torch.bfloat16)
+    h0 = state.clone()
+    t = _inputs(bsz, nh, p_, n, ng, 6)
+    out = ms.selective_state_update(state, **_to(t, gpu), dt_softplus=True)
+    for b in (0, 37, 63):
+        sl = slice(b, b + 1)
+        sub = {k: (v[sl] if k in ("x", "dt", "B", "C") else v) for k, v in t.items() if v is not None}
+        ref_h, ref_y = omx.update_math(h0[sl].float().cpu(), sub["x"], sub["dt"], sub["A"],
+                                       sub["B"], sub["C"], sub["D"], None, sub["dt_bias"], True)
+        _assert_state_ulp(state[sl], ref_h.to(torch.bfloat16))
+        assert_close_rel(out[sl].float().cpu(), ref_y.to(torch.bfloat16).float(), rtol=8e-3,
+                         what=f"y batch {b}")
+
+
+def test_drift_tool_replays_on_the_oracle(gpu):
+    """layer_quant_amd.drift on a short chain (batch 1, 6 steps): the reported drift of the MX4
+    state, the bf16 state and y agrees with the same chain replayed through the CPU oracle."""
+    import numpy as np
+
+    from layer_quant_amd import drift
+
+    rec = {}
+    res = drift.run(batch=1, steps=6, checkpoints=(3, 6), record=rec)
+    assert [r["step"] for r in res["drift"]] == [3, 6]
+    q, e, m = omx.mx_encode(rec["h0"].numpy(), 4, omx.ROUND_NEAREST_EVEN)
+    hb = rec["h0"].to(torch.bfloat16)
+    hf = rec["h0"].clone()
+    total = rec["h0"].numel()
+    got = {}
+    for i, s in enumerate(rec["steps"], start=1):
+        q, e, m, y4, _ = omx.mx_update(q, e, m, s["x"], s["dt"], rec["A"], s["B"], s["C"],
+                                       D=rec["D"], format_bits=4,
+                                       round_mode=omx.ROUND_SR_COUNTER, seed=1234,
+                                       rng_offset=(i - 1) * total)
+        hb, yb = omx.bf16_state_update(hb, s["x"], s["dt"], rec["A"], s["B"], s["C"], rec["D"])
+        hf, _ = omx.update_math(hf, s["x"], s["dt"], rec["A"], s["B"], s["C"], rec["D"])
+        if i in (3, 6):
+            deq = torch.from_numpy(omx.mx_decode(q, e, m)).double()
+            got[i] = dict(
+                mx4_state_vs_bf16=((deq - hb.double()).norm() / hb.double().norm()).item(),
+                mx4_y_vs_bf16=((y4.to(torch.bfloat16).double() - yb.to(torch.bfloat16).double())
+                               .norm() / yb.to(torch.bfloat16).double().norm()).item(),
+                bf16_state_vs_fp32=((hb.double() - hf.double()).norm() / hf.double().norm())
+                .item())
+    for row in res["drift"]:
+        ref = got[row["step"]]
+        for k, v in ref.items():
+            assert np.isfinite(row[k])
+            assert abs(row[k] - v) <= 0.05 * v + 1e-6, (row["step"], k, row[k], v)
