@@ -47,6 +47,11 @@ def parse_args():
     ap.add_argument("--mamba-layers", type=int, default=24)
     ap.add_argument("--state-bits", type=int, default=4, choices=[4, 8])
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    ap.add_argument("--sweep", action="store_true",
+                    help="instead of the decode step, time each kernel alone over the BASELINE "
+                         "configurations (attention: batch 1/8/64 x ctx 1K/4K/16K; MX8, MX4 and "
+                         "bf16 state updates: batch 1/8/64), each call after a 512 MB scratch "
+                         "read so that nothing is cache-resident; prints one JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy, the reference kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -78,8 +83,7 @@ class Events:
 
 def build_workload(torch, args, dev):
     from layer_quant_amd import _abi
-    from oracle.int4_kv import algorithmic_bytes, pack_algorithmic_bytes
-    from oracle.mx_state import update_algorithmic_bytes
+    from layer_quant_amd.traffic import attention_bytes, mx_update_bytes, pack_bytes
 
     B, S, g = args.batch, args.ctx, args.group
     hq, hkv, d = 32, 8, 128
@@ -126,9 +130,9 @@ def build_workload(torch, args, dev):
         mamba.append(layer)
     torch.cuda.synchronize()
     sizes = dict(
-        attention=algorithmic_bytes(B, hq, hkv, d, S, g),
-        pack=pack_algorithmic_bytes(B, hkv, 1, d, g),
-        mx_update=update_algorithmic_bytes(B, nh, p_, n, ng),
+        attention=attention_bytes(B, hq, hkv, d, S, g),
+        pack=pack_bytes(B, hkv, 1, d, g),
+        mx_update=mx_update_bytes(B, nh, p_, n, ng),
     )
     return attn, mamba, sizes
 
@@ -157,6 +161,88 @@ def run_step(torch, args, attn, mamba, ev=None):
             *M["st"], M["x"], M["dt"], M["dt_bias"], M["A"], M["B"], M["C"], M["D"], None,
             M["out"], args.state_bits, True, _abi.ROUND_SR_COUNTER, seed=1234, rng_offset=off))
         M["step"] += 1
+
+
+def sweep(torch, dev, reps: int = 20):
+    """Per-kernel cold-cache timings over the BASELINE configurations."""
+    from layer_quant_amd import _abi
+    from layer_quant_amd.traffic import attention_bytes, mx_update_bytes, ssm_update_bytes
+
+    scratch = torch.ones(512 << 20, dtype=torch.uint8, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    cache_bytes = 256 << 20
+
+    def timed(fn):
+        fn()
+        ts = []
+        for i in range(reps):
+            scratch.max()  # reads 512 MB: evicts L2 and the Infinity Cache, leaves no dirty lines
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            ts.append((a, b))
+        torch.cuda.synchronize()
+        us = sorted(1000.0 * a.elapsed_time(b) for a, b in ts)
+        return us[len(us) // 2], sum(us) / len(us)
+
+    def row(kernel, nbytes, med, mean, **cfg):
+        gbs = nbytes / (med * 1e-6) / 1e9
+        r = dict(kernel=kernel, **cfg, median_us=round(med, 2), mean_us=round(mean, 2),
+                 algorithmic_bytes=nbytes, GB_s=round(gbs, 1),
+                 frac_of_peak=round(gbs / PEAK_HBM_GBS, 4), fits_in_infinity_cache=nbytes <= cache_bytes)
+        log(f"{kernel} {cfg}: {med:.1f} us, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%})")
+        return r
+
+    rows = []
+    hq, hkv, d, g = 32, 8, 128, 32
+    for B in (1, 8, 64):
+        for S in (1024, 4096, 16384):
+            kp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
+            vp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
+            ks = torch.rand(B, hkv, S, d // g, device=dev, generator=gen) + 0.01
+            vs = torch.rand(B, hkv, S, d // g, device=dev, generator=gen) + 0.01
+            q = torch.randn(B, hq, 1, d, device=dev, generator=gen).to(torch.bfloat16)
+            out = torch.empty(B, hq, d, device=dev, dtype=torch.bfloat16)
+            med, mean = timed(lambda: _abi.int4_decode_attention(q, kp, vp, ks, vs, None, out, S, 4, g))
+            rows.append(row("int4_decode_attention", attention_bytes(B, hq, hkv, d, S, g), med, mean,
+                            batch=B, ctx=S, group=g))
+            del kp, vp, ks, vs
+    nh, p_, n, ng = 128, 64, 128, 8
+    for B in (1, 8, 64):
+        x = torch.randn(B, nh, p_, device=dev, generator=gen).to(torch.bfloat16)
+        dt = torch.randn(B, nh, device=dev, generator=gen).to(torch.bfloat16)[:, :, None].expand(B, nh, p_)
+        A = (-torch.exp(torch.rand(nh, device=dev, generator=gen) * 2))[:, None, None].expand(nh, p_, n)
+        Bm = torch.randn(B, ng, n, device=dev, generator=gen).to(torch.bfloat16)
+        Cm = torch.randn(B, ng, n, device=dev, generator=gen).to(torch.bfloat16)
+        D = torch.randn(nh, device=dev, generator=gen)[:, None].expand(nh, p_)
+        dtb = (torch.randn(nh, device=dev, generator=gen) * 0.1)[:, None].expand(nh, p_)
+        out = torch.empty(B, nh, p_, device=dev, dtype=torch.bfloat16)
+        h0 = torch.randn(B, nh, p_, n, device=dev, generator=gen) * 0.5
+        for bits in (8, 4):
+            st = (torch.empty(B, nh, p_, n, dtype=torch.int8, device=dev),
+                  torch.empty(B, nh, p_, n // 16, dtype=torch.uint8, device=dev),
+                  torch.empty(B, nh, p_, n // 2, dtype=torch.uint8, device=dev))
+            _abi.mx_encode(h0, *st, bits, _abi.ROUND_NEAREST_EVEN)
+            step = [0]
+
+            def upd():
+                _abi.mx_state_update(*st, x, dt, dtb, A, Bm, Cm, D, None, out, bits, True,
+                                     _abi.ROUND_SR_COUNTER, seed=1234,
+                                     rng_offset=step[0] * B * nh * p_ * n)
+                step[0] += 1
+            med, mean = timed(upd)
+            rows.append(row(f"mx{bits}_state_update", mx_update_bytes(B, nh, p_, n, ng), med, mean,
+                            batch=B, rounding="stochastic (counter)"))
+        state = h0.to(torch.bfloat16)
+        med, mean = timed(lambda: _abi.selective_state_update(state, x, dt, dtb, A, Bm, Cm, D, None,
+                                                              out, True))
+        rows.append(row("bf16_selective_state_update", ssm_update_bytes(B, nh, p_, n, ng), med, mean,
+                        batch=B))
+    return {"sweep": rows, "reps": reps, "timing": "median of per-call HIP events, each call after a "
+            "512 MB scratch read (a read evicts the caches without leaving dirty lines whose "
+            "write-back would compete with the timed kernel)", "peak_GB_s": PEAK_HBM_GBS}
 
 
 def cpu_baseline(args):
@@ -256,6 +342,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.sweep:
+        print(json.dumps(sweep(torch, dev)), flush=True)
+        return
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)

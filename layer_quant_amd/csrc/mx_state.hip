@@ -492,22 +492,6 @@ __global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
   if (L.active) store_block<VEC>(qp, mp, ep, qw, mw, eo_bits);
 }
 
-// Row-sum over the 2^BPR_LOG2 adjacent lanes of a state row with DPP moves: quad swaps, then the
-// half-row mirror (lane i <-> 7 - i) and the row mirror (i <-> 15 - i), each pairing every lane
-// with one in the other half of its group.
-template <int BPR_LOG2>
-__device__ __forceinline__ float row_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
-  if constexpr (BPR_LOG2 >= 3) {
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
-  }
-  if constexpr (BPR_LOG2 >= 4) {
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
-  }
-  return v;
-}
-
 // Update of the model's decode call (ms.py:97-222, 289-544 for the Nemotron-H layout): state rows
 // contiguous (row stride N), B and C bf16 with a contiguous d_state, and dt, dt_bias, A and D
 // constant within a head (stride 0 along head_dim, A also along d_state), as the model passes
@@ -561,47 +545,6 @@ __device__ __forceinline__ void load_rows(const MxUpdateParams& p, const HeadBuf
     L.xw[r] = __builtin_amdgcn_raw_buffer_load_b32(hb.x, (pc * p.x_row_bytes) & ~3u, 0, 0);
     L.zw[r] = __builtin_amdgcn_raw_buffer_load_b32(hb.z, (pc * p.z_row_bytes) & ~3u, 0, 0);
   }
-}
-
-// 16 bf16 values of B or C for the lane's block column (two 16-byte loads).
-__device__ __forceinline__ void load_bc(const MxUpdateParams& p, int b, int grp, uint32_t n0,
-                                        uint32_t N, u32x4_t (&bw)[2], u32x4_t (&cw)[2]) {
-  const auto rB = make_buf(vbase(p.B, b, grp), N * 2);
-  const auto rC = make_buf(vbase(p.C, b, grp), N * 2);
-  bw[0] = __builtin_amdgcn_raw_buffer_load_b128(rB, n0 * 2, 0, 0);
-  bw[1] = __builtin_amdgcn_raw_buffer_load_b128(rB, n0 * 2 + 16, 0, 0);
-  cw[0] = __builtin_amdgcn_raw_buffer_load_b128(rC, n0 * 2, 0, 0);
-  cw[1] = __builtin_amdgcn_raw_buffer_load_b128(rC, n0 * 2 + 16, 0, 0);
-}
-
-__device__ __forceinline__ void expand_bf16(const u32x4_t (&w)[2], float (&o)[16]) {
-  const uint32_t a[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    o[2 * i] = __uint_as_float(a[i] << 16);
-    o[2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
-  }
-}
-
-// Head scalars (ms.py:134-139): dt (+ dt_bias, softplus), exp(A dt) and D of head h. Without
-// dt_bias or D the host points their views at dt with zero strides, so every scalar load is
-// unconditional. exp and log use the hardware transcendentals (relative error ~1e-6, far inside
-// the 2e-3 output tolerance).
-struct HeadScalars {
-  float dt, dA, D;
-};
-
-__device__ __forceinline__ HeadScalars head_scalars(const MxUpdateParams& p, int b, int h) {
-  HeadScalars s;
-  float dtv = uniform_elem(vbase(p.dt, b, h), p.dt.dtype);
-  const float dtb = uniform_elem(vbase(p.dtb, h, 0), p.dtb.dtype);
-  const float av = uniform_elem(vbase(p.A, h, 0), p.A.dtype);
-  s.D = uniform_elem(vbase(p.D, h, 0), p.D.dtype);
-  if (p.has_dtb) dtv += dtb;
-  if (p.softplus) dtv = dtv <= 20.0f ? __logf(1.0f + __expf(dtv)) : dtv;
-  s.dt = dtv;
-  s.dA = __expf(av * dtv);
-  return s;
 }
 
 // Update, y, and writeback encode of the R rows held in L.

@@ -11,17 +11,26 @@
 // Geometry as the MX general kernel: one lane per 16-value block of a state row, the N/16 block
 // lanes of a row adjacent, grid (ceil(P * vbpr / 256), H, B).
 #include <math.h>
+#include <stdlib.h>
 
 #include "lq_common.h"
 #include "state_common.h"
 
 namespace lq {
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
 struct SsmParams {
   View st, x, dt, dtb, A, B, C, D, z, out;
   int Bn, H, P, N, ratio, bpr, vbpr_log2;
   int has_dtb, has_D, has_z, softplus, a_row_const;
   uint32_t st_span;  // bytes of one (batch, head) state slice, for the vector path's descriptor
+  // rows kernel: byte stride between rows of x, z and out, and the byte span of one
+  // (batch, head) slice of each rounded up to 4 (0 for an absent z)
+  uint32_t x_row_bytes, z_row_bytes, out_row_bytes;
+  uint32_t x_span, z_span, out_span;
 };
 
 // 16 state values of one lane: buffer loads for a contiguous 16-byte aligned last dimension
@@ -151,6 +160,157 @@ __global__ __launch_bounds__(256) void ssm_update_kernel(SsmParams p) {
     store_float((char*)vbase(p.out, b, h), p.out.dtype, pp * p.out.s[2], y);
   }
   if (L.active) store_state16<SDT, VEC>(p, sb, pp, n0, hv);
+}
+
+// Rows kernel for the model's decode call: state rows contiguous (row stride N) in 16-byte
+// aligned (batch, head) slices, B and C bf16 with a contiguous d_state, dt, dt_bias, A and D
+// constant within a head. 256 threads; lane (slot, blk) owns rows slot and slot + SLOTS, and in
+// each row the 16-byte chunks blk, blk + BPR, ... (VPC = 16 / sizeof(state) values each), so that
+// every load and store instruction of a wave covers whole consecutive rows. Every load of the lane
+// (its state chunks, x, z, B, C, the head scalars) is issued before the first use of any of them,
+// through per-(batch, head) buffer descriptors with the streaming state policy; the state goes
+// back with the hardware round-to-nearest-even converts.
+constexpr int SSM_ROWS = 2;
+
+template <int SDT, int BPR_LOG2>
+__global__ __launch_bounds__(256) void ssm_update_rows_kernel(SsmParams p) {
+  constexpr int BPR = 1 << BPR_LOG2;
+  constexpr uint32_t N = 16 * BPR;
+  constexpr int SLOTS = 256 >> BPR_LOG2;
+  constexpr int R = SSM_ROWS;
+  constexpr uint32_t ES = SDT == LQ_F32 ? 4 : 2;
+  constexpr int VPC = 16 / ES;     // state values per 16-byte chunk
+  constexpr int NCH = 16 / VPC;    // chunks per lane and row
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int blk = threadIdx.x & (BPR - 1);
+  const int slot = threadIdx.x >> BPR_LOG2;
+  const int P = p.P;
+  const int row0 = blockIdx.x * (R * SLOTS);
+
+  const auto rs = make_buf(vbase(p.st, b, h), (uint32_t)P * N * ES);
+  const auto rx = make_buf(vbase(p.x, b, h), p.x_span);
+  const auto rz = make_buf(vbase(p.z, b, h), p.z_span);  // span 0 without z: loads return 0
+  u32x4_t sw[R][NCH];
+  uint32_t xw[R], zw[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t pc = (uint32_t)min(row0 + r * SLOTS + slot, P - 1);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      sw[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, pc * N * ES + (j * BPR + blk) * 16u, 0,
+                                                       STATE_LOAD_POLICY);
+    }
+    xw[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, (pc * p.x_row_bytes) & ~3u, 0, 0);
+    zw[r] = __builtin_amdgcn_raw_buffer_load_b32(rz, (pc * p.z_row_bytes) & ~3u, 0, 0);
+  }
+  // B and C at the lane's d_state positions: VPC bf16 values per chunk (16 or 8 bytes)
+  const int grp = h / p.ratio;
+  const auto rB = make_buf(vbase(p.B, b, grp), N * 2);
+  const auto rC = make_buf(vbase(p.C, b, grp), N * 2);
+  uint32_t bw[8], cw[8];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const uint32_t off = (uint32_t)(j * BPR + blk) * VPC * 2u;
+    if constexpr (VPC == 8) {
+      const u32x4_t vb = __builtin_amdgcn_raw_buffer_load_b128(rB, off, 0, 0);
+      const u32x4_t vc = __builtin_amdgcn_raw_buffer_load_b128(rC, off, 0, 0);
+      bw[4 * j] = vb.x; bw[4 * j + 1] = vb.y; bw[4 * j + 2] = vb.z; bw[4 * j + 3] = vb.w;
+      cw[4 * j] = vc.x; cw[4 * j + 1] = vc.y; cw[4 * j + 2] = vc.z; cw[4 * j + 3] = vc.w;
+    } else {
+      const u32x2_t vb = __builtin_amdgcn_raw_buffer_load_b64(rB, off, 0, 0);
+      const u32x2_t vc = __builtin_amdgcn_raw_buffer_load_b64(rC, off, 0, 0);
+      bw[2 * j] = vb.x; bw[2 * j + 1] = vb.y;
+      cw[2 * j] = vc.x; cw[2 * j + 1] = vc.y;
+    }
+  }
+  const HeadScalars hs = head_scalars(p, b, h);
+  float Bd[16], Cv[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    Bd[2 * i] = __uint_as_float(bw[i] << 16) * hs.dt;
+    Bd[2 * i + 1] = __uint_as_float(bw[i] & 0xffff0000u) * hs.dt;
+    Cv[2 * i] = __uint_as_float(cw[i] << 16);
+    Cv[2 * i + 1] = __uint_as_float(cw[i] & 0xffff0000u);
+  }
+  const auto ro = make_buf(vbase(p.out, b, h), p.out_span);
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int pp = row0 + r * SLOTS + slot;
+    const bool act = pp < P;
+    const uint32_t pc = (uint32_t)min(pp, P - 1);
+    const float xv = word_elem(xw[r], ((pc * p.x_row_bytes) & 2u) * 8u, p.x.dtype);
+    float hv[16];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const uint32_t a[4] = {sw[r][j].x, sw[r][j].y, sw[r][j].z, sw[r][j].w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        if constexpr (SDT == LQ_F32) {
+          hv[4 * j + w] = __uint_as_float(a[w]);
+        } else {
+          hv[8 * j + 2 * w] = word_elem(a[w], 0, SDT);
+          hv[8 * j + 2 * w + 1] = word_elem(a[w], 16, SDT);
+        }
+      }
+    }
+    float ypart = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      hv[i] = fmaf(hv[i], hs.dA, Bd[i] * xv);
+      ypart = fmaf(hv[i], Cv[i], ypart);
+    }
+    float y = row_sum<BPR_LOG2>(ypart);
+    if (p.has_D) y += xv * hs.D;
+    if (p.has_z) {
+      const float zv = word_elem(zw[r], ((pc * p.z_row_bytes) & 2u) * 8u, p.z.dtype);
+      y *= zv / (1.0f + __expf(-zv));
+    }
+    if (act && blk == 0) {
+      const uint32_t oo = (uint32_t)pp * p.out_row_bytes;
+      if (p.out.dtype == LQ_F32) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), ro, oo, 0, 0);
+      } else if (p.out.dtype == LQ_BF16) {
+        __builtin_amdgcn_raw_buffer_store_b16(float_to_bf16_bits(y), ro, oo, 0, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)y), ro, oo,
+                                              0, 0);
+      }
+    }
+    if (act) {
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        u32x4_t w;
+        if constexpr (SDT == LQ_F32) {
+          w = u32x4_t{__float_as_uint(hv[4 * j]), __float_as_uint(hv[4 * j + 1]),
+                      __float_as_uint(hv[4 * j + 2]), __float_as_uint(hv[4 * j + 3])};
+        } else {
+          uint32_t o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x2_t v2{hv[8 * j + 2 * i], hv[8 * j + 2 * i + 1]};
+            if constexpr (SDT == LQ_BF16) {
+              o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v2, bf16x2_t));
+            } else {
+              o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v2, f16x2_t));
+            }
+          }
+          w = u32x4_t{o[0], o[1], o[2], o[3]};
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(w, rs, (uint32_t)pp * N * ES + (j * BPR + blk) * 16u,
+                                               0, STATE_STORE_POLICY);
+      }
+    }
+  }
+}
+
+template <int SDT>
+static void launch_ssm_rows(const SsmParams& p, dim3 grid, hipStream_t st) {
+  switch (p.vbpr_log2) {
+    case 2: hipLaunchKernelGGL((ssm_update_rows_kernel<SDT, 2>), grid, dim3(256), 0, st, p); break;
+    case 3: hipLaunchKernelGGL((ssm_update_rows_kernel<SDT, 3>), grid, dim3(256), 0, st, p); break;
+    default: hipLaunchKernelGGL((ssm_update_rows_kernel<SDT, 4>), grid, dim3(256), 0, st, p); break;
+  }
 }
 
 template <int SDT>
@@ -289,9 +449,48 @@ extern "C" int lq_selective_state_update(const lq_tensor* state, const lq_tensor
            t->stride[0] % 8 == 0 && t->stride[1] % 8 == 0;
   };
   const bool bcvec = bcv(B) && bcv(C);
+  hipStream_t s = (hipStream_t)stream;
+  const char* force = getenv("LQ_SSM_FORCE_GENERIC");
+  const bool forced = force != nullptr && force[0] != '\0' && force[0] != '0';
+  const int64_t lim = (int64_t)1 << 28;
+  const bool rows_ok =
+      !forced && vec && bcvec && (N == 64 || N == 128 || N == 256) && state->stride[2] == N &&
+      dt->stride[2] == 0 && A->stride[1] == 0 && A->stride[2] == 0 &&
+      (dt_bias == nullptr || dt_bias->stride[1] == 0) && (D == nullptr || D->stride[1] == 0) &&
+      x->stride[2] >= 0 && out->stride[2] >= 0 && (z == nullptr || z->stride[2] >= 0) &&
+      P * x->stride[2] < lim && P * out->stride[2] < lim && (z == nullptr || P * z->stride[2] < lim) &&
+      P * N * es < ((int64_t)1 << 31);
+  if (rows_ok) {
+    auto row_bytes = [](const View& v) { return (uint32_t)(v.s[2] * dtype_size(v.dtype)); };
+    auto span = [&](const View& v) {
+      return (uint32_t)((((P - 1) * v.s[2] + 1) * dtype_size(v.dtype) + 3) & ~(int64_t)3);
+    };
+    p.x_row_bytes = row_bytes(p.x);
+    p.x_span = span(p.x);
+    p.out_row_bytes = row_bytes(p.out);
+    p.out_span = span(p.out);
+    if (p.has_z) {
+      p.z_row_bytes = row_bytes(p.z);
+      p.z_span = span(p.z);
+    } else {  // a zero-span descriptor on x: its loads return 0 without reading memory
+      p.z = p.x;
+      p.z_row_bytes = 0;
+      p.z_span = 0;
+    }
+    const View dt0{p.dt.data, p.dt.dtype, {0, 0, 0, 0}};
+    if (!p.has_dtb) p.dtb = dt0;
+    if (!p.has_D) p.D = dt0;
+    const int rows = SSM_ROWS * (256 >> p.vbpr_log2);
+    const dim3 rgrid((unsigned)((P + rows - 1) / rows), (unsigned)H, (unsigned)Bn);
+    switch (state->dtype) {
+      case LQ_BF16: launch_ssm_rows<LQ_BF16>(p, rgrid, s); break;
+      case LQ_F16: launch_ssm_rows<LQ_F16>(p, rgrid, s); break;
+      default: launch_ssm_rows<LQ_F32>(p, rgrid, s); break;
+    }
+    return check_launch("lq_selective_state_update");
+  }
   const int64_t lanes = P << p.vbpr_log2;
   const dim3 grid((unsigned)((lanes + 255) / 256), (unsigned)H, (unsigned)Bn);
-  hipStream_t s = (hipStream_t)stream;
   switch (state->dtype) {
     case LQ_BF16: launch_ssm<LQ_BF16>(p, vec, bcvec, grid, s); break;
     case LQ_F16: launch_ssm<LQ_F16>(p, vec, bcvec, grid, s); break;

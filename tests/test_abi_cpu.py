@@ -122,3 +122,38 @@ def test_compute_wrappers_refuse_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU only"):
         _abi.int4_pack_kv(x, torch.zeros(1, 1, 4, 64, dtype=torch.uint8), torch.zeros(1, 1, 4, 4),
                           torch.zeros(1, dtype=torch.long), 32)
+
+
+def test_selective_state_update_rejects_bad_arguments():
+    lib = _abi.lib()
+    st = _fake((2, 4, 8, 128), torch.bfloat16)
+    x = _fake((2, 4, 8), torch.bfloat16)
+    A = _fake((4, 8, 128), torch.float32)
+    B = _fake((2, 2, 128), torch.bfloat16)
+    out = _fake((2, 4, 8), torch.bfloat16)
+    assert lib.lq_selective_state_update(None, x, x, None, A, B, B, None, None, out, 1,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+    st_int = _fake((2, 4, 8, 128), torch.int8)
+    assert lib.lq_selective_state_update(st_int, x, x, None, A, B, B, None, None, out, 1,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+    assert "not f32/f16/bf16" in _abi.last_error()
+    st40 = _fake((2, 4, 8, 40), torch.bfloat16)
+    assert lib.lq_selective_state_update(st40, x, x, None, A, B, B, None, None, out, 1,
+                                         None) == _abi.LQ_ERR_UNSUPPORTED
+    assert "multiple of 16" in _abi.last_error()
+    bad_dt = _fake((2, 4, 9), torch.bfloat16)
+    assert lib.lq_selective_state_update(st, x, bad_dt, None, A, B, B, None, None, out, 1,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+    assert "dt must be [2, 4, 8]" in _abi.last_error()
+    B3 = _fake((2, 3, 128), torch.bfloat16)
+    assert lib.lq_selective_state_update(st, x, x, None, A, B3, B3, None, None, out, 1,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+    assert "not divisible by ngroups=3" in _abi.last_error()
+    D_bad = _fake((4, 7), torch.float32)
+    assert lib.lq_selective_state_update(st, x, x, None, A, B, B, D_bad, None, out, 1,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+    with pytest.raises(RuntimeError, match="GPU only"):
+        _abi.selective_state_update(torch.zeros(1, 1, 1, 16), torch.zeros(1, 1, 1),
+                                    torch.zeros(1, 1, 1), None, torch.zeros(1, 1, 16),
+                                    torch.zeros(1, 1, 16), torch.zeros(1, 1, 16), None, None,
+                                    torch.zeros(1, 1, 1), False)

@@ -38,6 +38,14 @@ def _inputs(bsz, nh, p_, n, ng, seed, head_const=True, z=False, dt_zero=False):
     )
 
 
+@pytest.fixture(params=["rows", "general"])
+def path(request, monkeypatch):
+    """Run a model-layout test on the row kernel, and once more with the general kernel forced."""
+    if request.param == "general":
+        monkeypatch.setenv("LQ_SSM_FORCE_GENERIC", "1")
+    return request.param
+
+
 def _to(t, dev):
     return {k: (None if v is None else v.to(dev)) for k, v in t.items()}
 
@@ -64,7 +72,7 @@ def _assert_state_ulp(got: torch.Tensor, ref: torch.Tensor, frac=0.999):
 
 @pytest.mark.parametrize("sdtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("n", [64, 128, 256])
-def test_update_model_layout(gpu, sdtype, n):
+def test_update_model_layout(gpu, path, sdtype, n):
     bsz, nh, p_, ng = 3, 16, 32, 4
     g = torch.Generator().manual_seed(n)
     h0 = (torch.randn(bsz, nh, p_, n, generator=g) * 0.5).to(sdtype)
@@ -105,7 +113,7 @@ def test_update_general_layout_z_f32_out(gpu):
     assert torch.equal(big.to(gpu)[:, :, p_:].cpu(), big[:, :, p_:])
 
 
-def test_dt_zero_keeps_state(gpu):
+def test_dt_zero_keeps_state(gpu, path):
     bsz, nh, p_, n, ng = 2, 8, 64, 128, 8
     g = torch.Generator().manual_seed(11)
     h0 = (torch.randn(bsz, nh, p_, n, generator=g) * 0.5).to(torch.bfloat16)
@@ -141,7 +149,7 @@ def test_headless_forms_match(gpu):
     assert torch.equal(y3, y4[:, 0]) and torch.equal(s3, s4[:, 0])
 
 
-def test_full_size_b64_model_layout(gpu):
+def test_full_size_b64_model_layout(gpu, path):
     """Nemotron-H layer at batch 64 (128 heads x 64 x 128, 8 groups): three sampled batch rows
     against the oracle's fp32 update, the state within one bf16 ulp of its rounding."""
     bsz, nh, p_, n, ng = 64, 128, 64, 128, 8

@@ -174,3 +174,11 @@ def test_decode_attention_mask_branches():
 def test_algorithmic_bytes_headline_figure():
     # B=64, ctx 16384, group 32, bf16 q and out: the figure quoted for the headline config
     assert ik.algorithmic_bytes(64, 32, 8, 128, 16384, 32) == 1_343_225_856
+
+
+def test_package_byte_counts_match_the_oracle():
+    from layer_quant_amd import traffic
+
+    for args in [(64, 32, 8, 128, 16384, 32), (1, 32, 8, 128, 1024, 32), (8, 32, 8, 128, 4096, 64)]:
+        assert traffic.attention_bytes(*args) == ik.algorithmic_bytes(*args)
+    assert traffic.pack_bytes(64, 8, 1, 128, 32) == ik.pack_algorithmic_bytes(64, 8, 1, 128, 32)

@@ -256,3 +256,13 @@ def test_rng_bijective_and_uniform():
 
 def test_algorithmic_bytes_headline_figure():
     assert mx.update_algorithmic_bytes(64, 128, 64, 128, 8) == 212_092_416
+
+
+def test_package_byte_counts_match_the_oracle():
+    from layer_quant_amd import traffic
+
+    for b in (1, 8, 64):
+        assert traffic.mx_update_bytes(b, 128, 64, 128, 8) == mx.update_algorithmic_bytes(b, 128, 64, 128, 8)
+    # the unquantized update moves 2 bytes per state element each way
+    assert traffic.ssm_update_bytes(64, 128, 64, 128, 8) - traffic.mx_update_bytes(64, 128, 64, 128, 8) \
+        == 2 * 64 * 128 * 64 * 128 * (2 - (1 + 1 / 16 + 1 / 2))
