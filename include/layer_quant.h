@@ -57,6 +57,15 @@ enum {
   LQ_ROUND_SR_UNIFORM = 2,   /* floor(q) + (u < q - floor(q)), u from a caller fp32 tensor       */
   LQ_ROUND_SR_COUNTER = 3    /* same comparison, u from the library's counter-based generator    */
 };
+/*
+ * The counter-based generator of LQ_ROUND_SR_COUNTER: element (b,h,p,n) draws counter
+ * c = rng_offset + ((b*H + h)*P + p)*N + n (the reference's tl.rand offsets, step*B*H*P*N + index,
+ * when rng_offset = step*B*H*P*N). With K = lowbias32(lo32(seed) ^ lowbias32(hi32(seed) ^
+ * 0x9E3779B9)) and W = lowbias32(lo32(c>>1) ^ lowbias32(hi32(c>>1) ^ K)), the draw is
+ * u16 = (W >> 16*(c&1)) & 0xFFFF, and the level is (trunc(v * 2^16 / pair_scale) + u16) >> 16 (a
+ * fixed-point dither that rounds up with probability floor(frac * 2^16) / 2^16).
+ * lowbias32(x): x ^= x>>16; x *= 0x7feb352d; x ^= x>>15; x *= 0x846ca68b; x ^= x>>16.
+ */
 
 typedef struct lq_tensor {
   void* data;

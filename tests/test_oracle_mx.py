@@ -242,6 +242,30 @@ def test_rng_vectorized_matches_scalar_and_golden():
     assert rng.lowbias32_scalar(1) == golden["lowbias32"]["1"]
 
 
+def test_rng_adjacent_draws_uncorrelated():
+    """Draws of neighbouring counters -- the two halves of one hashed word, adjacent pairs and
+    pairs further apart -- show no correlation: lag correlations within 5 sigma of zero and a
+    2-D chi-square of (u_n, u_{n+lag}) on a 16x16 grid within its 0.9999 quantile."""
+    n = 1 << 21
+    u = rng.uniforms_u16(1234, np.arange(n, dtype=np.uint64) + np.uint64(7 << 20)).astype(np.float64)
+    z = (u - u.mean()) / u.std()
+    for lag in (1, 2, 3, 8, 15, 16, 17, 32):
+        r = float(np.mean(z[:-lag] * z[lag:]))
+        assert abs(r) < 5 / np.sqrt(n), (lag, r)
+        a = (u[:-lag] / 4096).astype(np.int64)
+        b = (u[lag:] / 4096).astype(np.int64)
+        hist = np.bincount(a * 16 + b, minlength=256)
+        expected = hist.sum() / 256
+        chi2 = float(((hist - expected) ** 2 / expected).sum())
+        assert chi2 < 360, (lag, chi2)  # 255 dof: the 0.9999 quantile is about 351-360
+    # the draws at each position of a 16-value block, over many blocks, are uniform
+    u16 = u.reshape(-1, 16)
+    for j in range(16):
+        hist = np.bincount((u16[:, j] / 4096).astype(np.int64), minlength=16)
+        expected = hist.sum() / 16
+        assert float(((hist - expected) ** 2 / expected).sum()) < 50, j
+
+
 def test_rng_bijective_and_uniform():
     x = np.arange(1 << 20, dtype=np.uint32)
     y = rng.lowbias32(x)
