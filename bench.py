@@ -46,6 +46,9 @@ def parse_args():
     ap.add_argument("--attn-layers", type=int, default=4)
     ap.add_argument("--mamba-layers", type=int, default=24)
     ap.add_argument("--state-bits", type=int, default=4, choices=[4, 8])
+    ap.add_argument("--state-layout", default="reference", choices=["reference", "compact"],
+                    help="MX cache layout: the reference's tensors (default) or the compact one "
+                         "(bit micro-exponents, MX4 nibble mantissas; same arithmetic)")
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--sweep", action="store_true",
                     help="instead of the decode step, time each kernel alone over the BASELINE "
@@ -81,6 +84,19 @@ class Events:
         return 1000.0 * sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
 
 
+def _mx_tensors(torch, shape, bits, layout, dev):
+    """Empty MX state tensors (q_state, shared_exp, micro_exp) in the given layout."""
+    b, h, p, n = shape
+    if layout == "compact":
+        q = torch.empty(b, h, p, n // 2 if bits == 4 else n,
+                        dtype=torch.uint8 if bits == 4 else torch.int8, device=dev)
+        m = torch.empty(b, h, p, n // 16, dtype=torch.uint8, device=dev)
+    else:
+        q = torch.empty(shape, dtype=torch.int8, device=dev)
+        m = torch.empty(b, h, p, n // 2, dtype=torch.uint8, device=dev)
+    return q, torch.empty(b, h, p, n // 16, dtype=torch.uint8, device=dev), m
+
+
 def build_workload(torch, args, dev):
     from layer_quant_amd import _abi
     from layer_quant_amd.traffic import attention_bytes, mx_update_bytes, pack_bytes
@@ -108,9 +124,7 @@ def build_workload(torch, args, dev):
     mamba = []
     for _ in range(args.mamba_layers):
         h0 = torch.randn(B, nh, p_, n, device=dev, generator=gen) * 0.5
-        st = (torch.empty(B, nh, p_, n, dtype=torch.int8, device=dev),
-              torch.empty(B, nh, p_, n // 16, dtype=torch.uint8, device=dev),
-              torch.empty(B, nh, p_, n // 2, dtype=torch.uint8, device=dev))
+        st = _mx_tensors(torch, (B, nh, p_, n), args.state_bits, args.state_layout, dev)
         _abi.mx_encode(h0, *st, args.state_bits, _abi.ROUND_NEAREST_EVEN)
         del h0
         layer = dict(
@@ -132,7 +146,8 @@ def build_workload(torch, args, dev):
     sizes = dict(
         attention=attention_bytes(B, hq, hkv, d, S, g),
         pack=pack_bytes(B, hkv, 1, d, g),
-        mx_update=mx_update_bytes(B, nh, p_, n, ng),
+        mx_update=mx_update_bytes(B, nh, p_, n, ng, format_bits=args.state_bits,
+                                  layout=args.state_layout),
     )
     return attn, mamba, sizes
 
@@ -220,10 +235,8 @@ def sweep(torch, dev, reps: int = 20):
         dtb = (torch.randn(nh, device=dev, generator=gen) * 0.1)[:, None].expand(nh, p_)
         out = torch.empty(B, nh, p_, device=dev, dtype=torch.bfloat16)
         h0 = torch.randn(B, nh, p_, n, device=dev, generator=gen) * 0.5
-        for bits in (8, 4):
-            st = (torch.empty(B, nh, p_, n, dtype=torch.int8, device=dev),
-                  torch.empty(B, nh, p_, n // 16, dtype=torch.uint8, device=dev),
-                  torch.empty(B, nh, p_, n // 2, dtype=torch.uint8, device=dev))
+        for bits, layout in ((8, "reference"), (4, "reference"), (8, "compact"), (4, "compact")):
+            st = _mx_tensors(torch, (B, nh, p_, n), bits, layout, dev)
             _abi.mx_encode(h0, *st, bits, _abi.ROUND_NEAREST_EVEN)
             step = [0]
 
@@ -233,8 +246,9 @@ def sweep(torch, dev, reps: int = 20):
                                      rng_offset=step[0] * B * nh * p_ * n)
                 step[0] += 1
             med, mean = timed(upd)
-            rows.append(row(f"mx{bits}_state_update", mx_update_bytes(B, nh, p_, n, ng), med, mean,
-                            batch=B, rounding="stochastic (counter)"))
+            rows.append(row(f"mx{bits}_state_update", mx_update_bytes(
+                B, nh, p_, n, ng, format_bits=bits, layout=layout), med, mean, batch=B,
+                layout=layout, rounding="stochastic (counter)"))
         state = h0.to(torch.bfloat16)
         med, mean = timed(lambda: _abi.selective_state_update(state, x, dt, dtb, A, Bm, Cm, D, None,
                                                               out, True))
@@ -387,7 +401,8 @@ def main():
         log(f"{name}: {us:.1f} us/call, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%})")
     dominant = max(kernels, key=lambda k: kernels[k]["us"] * kernels[k]["calls_per_step"])
     dk = kernels[dominant]
-    workload = f"b{args.batch}_ctx{args.ctx}_g{args.group}_mx{args.state_bits}"
+    workload = f"b{args.batch}_ctx{args.ctx}_g{args.group}_mx{args.state_bits}" + (
+        "_compact" if args.state_layout == "compact" else "")
     roofline = {
         "kernel": {"attention": "lq_int4_decode_attention (attn_fast_kernel, + attn_merge_kernel "
                                 "when split)",
@@ -422,11 +437,13 @@ def main():
                          f"INT4-KV attention layers (32q/8kv heads, head_dim 128, group "
                          f"{args.group}, ctx {args.ctx}) with their K/V packs + "
                          f"{args.mamba_layers} MX{args.state_bits} Mamba2 state updates "
-                         "(128 heads x 64 x 128, 8 groups, stochastic writeback)"),
+                         "(128 heads x 64 x 128, 8 groups, stochastic writeback"
+                         + (", compact cache layout)" if args.state_layout == "compact" else ")")),
             "batch": args.batch,
             "ctx": args.ctx,
             "group_size": args.group,
             "state_format": f"mx{args.state_bits}",
+            "state_layout": args.state_layout,
         },
         "kernels": kernels,
         "roofline": roofline,

@@ -26,6 +26,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "lq_common.h"
 #include "state_common.h"
 
@@ -62,6 +64,68 @@ struct MxCodecParams {
   uint32_t key;
   uint64_t rng_offset;
 };
+
+// State layouts: the reference's (one byte per mantissa, one byte per pair micro-exponent), and
+// the compact ones (micro-exponents as bits, bit k of byte j = pair 8j + k of the row; MX4
+// mantissas as two's-complement nibbles, byte p = value 2p in the low nibble, 2p + 1 in the high).
+// The exponent bytes are the reference's in all three.
+enum { LAYOUT_REF = 0, LAYOUT_CM8 = 1, LAYOUT_CM4 = 2 };
+template <int LY>
+struct LayoutOf {
+  static constexpr bool qnib = LY == LAYOUT_CM4;   // nibble mantissas
+  static constexpr bool mbits = LY != LAYOUT_REF;  // bit micro-exponents
+  static constexpr int qbytes = qnib ? 8 : 16;     // mantissa bytes per 16-value block
+  static constexpr int mbytes = mbits ? 1 : 8;     // micro-exponent bytes per block
+};
+
+// Mantissa n of a block's raw words, as float.
+template <int LY>
+__device__ __forceinline__ float mant(const uint32_t (&qw)[4], int n) {
+  if constexpr (LayoutOf<LY>::qnib) {
+    // the builtin's result type is unsigned: the signed field must be converted as an int
+    return (float)(int)__builtin_amdgcn_sbfe(qw[n >> 3], 4 * (n & 7), 4);
+  } else {
+    return (float)(int)(int8_t)(qw[n >> 2] >> (8 * (n & 3)));
+  }
+}
+
+// Micro-exponent of pair k of a block (the reference layout keeps the whole byte: e + micro
+// forms the scale exponent there).
+template <int LY>
+__device__ __forceinline__ uint32_t micro(const uint32_t (&mw)[2], int k) {
+  if constexpr (LayoutOf<LY>::mbits) {
+    return (mw[0] >> k) & 1u;
+  } else {
+    return (mw[k >> 2] >> (8 * (k & 3))) & 0xffu;
+  }
+}
+
+// Level bytes qw[4] (one int8 per value) and micro flags mb[8] (0/1) of an encoded block, in the
+// layout's raw form: nibbles qw[0..1] and micro bits mw[0] for the compact layouts.
+template <int LY>
+__device__ __forceinline__ void pack_block(uint32_t (&qw)[4], uint32_t (&mw)[2],
+                                           const uint32_t (&mb)[8]) {
+  if constexpr (LayoutOf<LY>::qnib) {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t ev = __builtin_amdgcn_perm(qw[2 * w + 1], qw[2 * w], 0x06040200u);
+      const uint32_t od = __builtin_amdgcn_perm(qw[2 * w + 1], qw[2 * w], 0x07050301u);
+      qw[w] = (ev & 0x0f0f0f0fu) | ((od << 4) & 0xf0f0f0f0u);
+    }
+    qw[2] = 0;
+    qw[3] = 0;
+  }
+  if constexpr (LayoutOf<LY>::mbits) {
+    uint32_t bits = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) bits |= mb[k] << k;
+    mw[0] = bits;
+    mw[1] = 0;
+  } else {
+    mw[0] = mb[0] | (mb[1] << 8) | (mb[2] << 16) | (mb[3] << 24);
+    mw[1] = mb[4] | (mb[5] << 8) | (mb[6] << 16) | (mb[7] << 24);
+  }
+}
 
 __device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
   x ^= x >> 16;
@@ -216,7 +280,7 @@ __device__ __forceinline__ float pair_maxima(const float (&v)[16], float (&pa)[8
 // supplied uniforms scaled by 2^16 (so that the comparison u < frac becomes u16 < frac * 2^16,
 // both sides exact), unused otherwise. The reference's final min(level, M) is omitted: every mode
 // already yields level <= M.
-template <int FB, int RMODE>
+template <int FB, int RMODE, int LY>
 __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16)[16],
                                          uint32_t (&qw)[4], uint32_t (&mw)[2], uint32_t& eb_out) {
 #pragma clang fp contract(off)
@@ -264,15 +328,14 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16
     const uint32_t hi = __builtin_amdgcn_perm((uint32_t)qi[4 * w + 3], (uint32_t)qi[4 * w + 2], 0x04000c0cu);
     qw[w] = lo | hi;
   }
-  mw[0] = mb[0] | (mb[1] << 8) | (mb[2] << 16) | (mb[3] << 24);
-  mw[1] = mb[4] | (mb[5] << 8) | (mb[6] << 16) | (mb[7] << 24);
+  pack_block<LY>(qw, mw, mb);
   eb_out = (uint32_t)eb;
 }
 
 // Encode 16 values in the counter mode: T = v * 2^(143 - se) with se = ebase + micro (one exact
 // fp32 scaling, = v / pair_scale * 2^16), clamped to +-M*2^16, truncated toward zero; the level
 // (T + u16) >> 16 is byte 2 of the 32-bit sum, which the packing picks directly.
-template <int FB>
+template <int FB, int LY>
 __device__ __forceinline__ void encode16_dither(const float (&v)[16], const uint32_t (&pw)[8],
                                                 uint32_t (&qw)[4], uint32_t (&mw)[2],
                                                 uint32_t& eb_out) {
@@ -312,29 +375,41 @@ __device__ __forceinline__ void encode16_dither(const float (&v)[16], const uint
     const uint32_t hi = __builtin_amdgcn_perm((uint32_t)sum[4 * w + 3], (uint32_t)sum[4 * w + 2], 0x06020c0cu);
     qw[w] = lo | hi;
   }
-  mw[0] = mb[0] | (mb[1] << 8) | (mb[2] << 16) | (mb[3] << 24);
-  mw[1] = mb[4] | (mb[5] << 8) | (mb[6] << 16) | (mb[7] << 24);
+  pack_block<LY>(qw, mw, mb);
   eb_out = (uint32_t)eb;
 }
 
-template <bool VEC>
+// Raw words of one block at q / mi / e (VEC: q and mi aligned to their block size).
+template <bool VEC, int LY>
 __device__ __forceinline__ void load_block(const int8_t* q, const uint8_t* mi, const uint8_t* e,
                                            uint32_t (&qw)[4], uint32_t (&mw)[2], uint32_t& ev) {
-  if constexpr (VEC) {
+  using L = LayoutOf<LY>;
+  const uint8_t* qb = (const uint8_t*)q;
+  qw[2] = qw[3] = 0;
+  mw[1] = 0;
+  if constexpr (VEC && L::qbytes == 16) {
     const uint4 a = *(const uint4*)q;
-    const uint2 m = *(const uint2*)mi;
     qw[0] = a.x;
     qw[1] = a.y;
     qw[2] = a.z;
     qw[3] = a.w;
+  } else if constexpr (VEC) {
+    const uint2 a = *(const uint2*)q;
+    qw[0] = a.x;
+    qw[1] = a.y;
+  } else {
+#pragma unroll
+    for (int w = 0; w < L::qbytes / 4; ++w) {
+      qw[w] = qb[4 * w] | (qb[4 * w + 1] << 8) | (qb[4 * w + 2] << 16) | ((uint32_t)qb[4 * w + 3] << 24);
+    }
+  }
+  if constexpr (L::mbits) {
+    mw[0] = *mi;
+  } else if constexpr (VEC) {
+    const uint2 m = *(const uint2*)mi;
     mw[0] = m.x;
     mw[1] = m.y;
   } else {
-    const uint8_t* qb = (const uint8_t*)q;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      qw[w] = qb[4 * w] | (qb[4 * w + 1] << 8) | (qb[4 * w + 2] << 16) | ((uint32_t)qb[4 * w + 3] << 24);
-    }
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
       mw[w] = mi[4 * w] | (mi[4 * w + 1] << 8) | (mi[4 * w + 2] << 16) | ((uint32_t)mi[4 * w + 3] << 24);
@@ -343,17 +418,25 @@ __device__ __forceinline__ void load_block(const int8_t* q, const uint8_t* mi, c
   ev = *e;
 }
 
-template <bool VEC>
+template <bool VEC, int LY>
 __device__ __forceinline__ void store_block(int8_t* q, uint8_t* mi, uint8_t* e,
                                             const uint32_t (&qw)[4], const uint32_t (&mw)[2],
                                             uint32_t ev) {
-  if constexpr (VEC) {
+  using L = LayoutOf<LY>;
+  uint8_t* qb = (uint8_t*)q;
+  if constexpr (VEC && L::qbytes == 16) {
     *(uint4*)q = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+  } else if constexpr (VEC) {
+    *(uint2*)q = make_uint2(qw[0], qw[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < L::qbytes; ++i) qb[i] = (uint8_t)(qw[i >> 2] >> (8 * (i & 3)));
+  }
+  if constexpr (L::mbits) {
+    *mi = (uint8_t)mw[0];
+  } else if constexpr (VEC) {
     *(uint2*)mi = make_uint2(mw[0], mw[1]);
   } else {
-    uint8_t* qb = (uint8_t*)q;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) qb[i] = (uint8_t)(qw[i >> 2] >> (8 * (i & 3)));
 #pragma unroll
     for (int i = 0; i < 8; ++i) mi[i] = (uint8_t)(mw[i >> 2] >> (8 * (i & 3)));
   }
@@ -362,19 +445,15 @@ __device__ __forceinline__ void store_block(int8_t* q, uint8_t* mi, uint8_t* e,
 
 // h_n = q_n * 2^(e - 127 + micro_pair(n)); the scale is built from exponent bits
 // (e + micro = 255 gives +inf, as exp2(128) does in fp32).
+template <int LY>
 __device__ __forceinline__ void decode16(const uint32_t (&qw)[4], const uint32_t (&mw)[2],
                                          uint32_t ev, float (&h)[16]) {
   const uint32_t evs = ev << 23;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    const uint32_t mi = (mw[k >> 2] >> (8 * (k & 3))) & 0xffu;
-    const float sc = __uint_as_float((mi << 23) + evs);
+    const float sc = __uint_as_float((micro<LY>(mw, k) << 23) + evs);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int n = 2 * k + i;
-      const int qv = (int)(int8_t)(qw[n >> 2] >> (8 * (n & 3)));
-      h[n] = (float)qv * sc;
-    }
+    for (int i = 0; i < 2; ++i) h[2 * k + i] = mant<LY>(qw, 2 * k + i) * sc;
   }
 }
 
@@ -396,7 +475,7 @@ __device__ __forceinline__ void block_u16(const View& uni, int b, int h, int pp,
 }
 
 // Writeback encode of one block in mode RMODE; c0 = counter of the block's first element.
-template <int FB, int RMODE>
+template <int FB, int RMODE, int LY>
 __device__ __forceinline__ void encode_block(const float (&v)[16], const View& uni, uint32_t key,
                                              uint64_t c0, int b, int h, int pp, int n0,
                                              uint32_t (&qw)[4], uint32_t (&mw)[2],
@@ -404,25 +483,35 @@ __device__ __forceinline__ void encode_block(const float (&v)[16], const View& u
   if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
     uint32_t pw[8];
     block_words(key, c0, pw);
-    encode16_dither<FB>(v, pw, qw, mw, eb);
+    encode16_dither<FB, LY>(v, pw, qw, mw, eb);
   } else {
     float u16[16];
     block_u16<RMODE>(uni, b, h, pp, n0, u16);
-    encode16<FB, RMODE>(v, u16, qw, mw, eb);
+    encode16<FB, RMODE, LY>(v, u16, qw, mw, eb);
   }
 }
 
-template <int FB, int RMODE, bool VEC, bool BCVEC>
+// Pointers to block blk of row pp of slice (b, h) in layout LY.
+template <int LY>
+__device__ __forceinline__ void block_ptrs(const MxState& st, int b, int h, int pp, int blk,
+                                           int8_t*& qp, uint8_t*& mp, uint8_t*& ep) {
+  using Lay = LayoutOf<LY>;
+  qp = st.q + (int64_t)b * st.qs[0] + (int64_t)h * st.qs[1] + pp * (int)st.qs[2] + blk * Lay::qbytes;
+  mp = st.mi + (int64_t)b * st.ms[0] + (int64_t)h * st.ms[1] + pp * (int)st.ms[2] + blk * Lay::mbytes;
+  ep = st.e + (int64_t)b * st.es[0] + (int64_t)h * st.es[1] + pp * (int)st.es[2] + blk;
+}
+
+template <int FB, int RMODE, bool VEC, bool BCVEC, int LY>
 __global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
   const LaneIdx L = lane_index(p.P, p.vbpr_log2, p.bpr);
   const int b = L.b, h = L.h, pp = L.pp;
   const int n0 = L.blk * 16;
 
-  int8_t* qp = p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1] + pp * (int)p.st.qs[2] + n0;
-  uint8_t* mp = p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1] + pp * (int)p.st.ms[2] + L.blk * 8;
-  uint8_t* ep = p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1] + pp * (int)p.st.es[2] + L.blk;
+  int8_t* qp;
+  uint8_t *mp, *ep;
+  block_ptrs<LY>(p.st, b, h, pp, L.blk, qp, mp, ep);
   uint32_t qw[4], mw[2], ev;
-  load_block<VEC>(qp, mp, ep, qw, mw, ev);
+  load_block<VEC, LY>(qp, mp, ep, qw, mw, ev);
 
   // per-row scalars (ms.py:134-139); exp and log use the hardware transcendentals (relative
   // error ~1e-6, far inside the 2e-3 output tolerance)
@@ -447,17 +536,15 @@ __global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
     const uint32_t evs = ev << 23;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const uint32_t mi = (mw[k >> 2] >> (8 * (k & 3))) & 0xffu;
-      const float sdA = __uint_as_float((mi << 23) + evs) * dA;
+      const float sdA = __uint_as_float((micro<LY>(mw, k) << 23) + evs) * dA;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int n = 2 * k + i;
-        const float qv = (float)(int)(int8_t)(qw[n >> 2] >> (8 * (n & 3)));
-        hv[n] = fmaf(qv, sdA, Bv[n] * dtx);
+        hv[n] = fmaf(mant<LY>(qw, n), sdA, Bv[n] * dtx);
       }
     }
   } else {
-    decode16(qw, mw, ev, hv);
+    decode16<LY>(qw, mw, ev, hv);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const float dA = __expf(ldf(ab, p.A.dtype, aoff + i * (int)p.A.s[2]) * dtv);
@@ -487,9 +574,9 @@ __global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
   // writeback encode (ms.py:168-222, 512-544)
   const uint64_t row = ((uint64_t)b * p.H + h) * p.P + pp;
   uint32_t eo_bits;
-  encode_block<FB, RMODE>(hv, p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0, b,
-                          h, pp, n0, qw, mw, eo_bits);
-  if (L.active) store_block<VEC>(qp, mp, ep, qw, mw, eo_bits);
+  encode_block<FB, RMODE, LY>(hv, p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0,
+                              b, h, pp, n0, qw, mw, eo_bits);
+  if (L.active) store_block<VEC, LY>(qp, mp, ep, qw, mw, eo_bits);
 }
 
 // Update of the model's decode call (ms.py:97-222, 289-544 for the Nemotron-H layout): state rows
@@ -508,8 +595,7 @@ __global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
 // State blocks and x words of R rows of one lane (the raw loads of one work item).
 template <int R>
 struct RowLoads {
-  u32x4_t q[R];
-  u32x2_t m[R];
+  uint32_t q[R][4], m[R][2];  // raw block words (layout-dependent, see LayoutOf)
   uint32_t e[R], xw[R], zw[R];
 };
 
@@ -518,12 +604,15 @@ struct HeadBufs {
   __amdgpu_buffer_rsrc_t q, m, e, x, z, out;
 };
 
-template <uint32_t N>
+template <uint32_t N, int LY>
 __device__ __forceinline__ HeadBufs head_bufs(const MxUpdateParams& p, int b, int h) {
+  using Lay = LayoutOf<LY>;
   HeadBufs hb;
   const uint32_t P = (uint32_t)p.P;
-  hb.q = make_buf(p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1], P * N);
-  hb.m = make_buf(p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1], P * (N / 2));
+  hb.q = make_buf(p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1],
+                  P * (N / 16) * Lay::qbytes);
+  hb.m = make_buf(p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1],
+                  P * (N / 16) * Lay::mbytes);
   hb.e = make_buf(p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1], P * (N / 16));
   hb.x = make_buf(vbase(p.x, b, h), p.x_span);
   hb.z = make_buf(vbase(p.z, b, h), p.z_span);  // span 0 without z: its loads return 0
@@ -532,15 +621,30 @@ __device__ __forceinline__ HeadBufs head_bufs(const MxUpdateParams& p, int b, in
 }
 
 // Issues the loads of rows row0 + r * SLOTS + slot (clamped to P - 1) of one slice.
-template <int R, int SLOTS, uint32_t N>
+// (qo = pc * N + n0 is the block's mantissa offset in the reference layout; every other offset is
+// a shift of it.)
+template <int R, int SLOTS, uint32_t N, int LY>
 __device__ __forceinline__ void load_rows(const MxUpdateParams& p, const HeadBufs& hb, int row0,
                                           int slot, uint32_t n0, RowLoads<R>& L) {
+  using Lay = LayoutOf<LY>;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const uint32_t pc = (uint32_t)min(row0 + r * SLOTS + slot, p.P - 1);
     const uint32_t qo = pc * N + n0;
-    L.q[r] = __builtin_amdgcn_raw_buffer_load_b128(hb.q, qo, 0, STATE_LOAD_POLICY);
-    L.m[r] = __builtin_amdgcn_raw_buffer_load_b64(hb.m, qo >> 1, 0, STATE_LOAD_POLICY);
+    if constexpr (Lay::qbytes == 16) {
+      const u32x4_t q4 = __builtin_amdgcn_raw_buffer_load_b128(hb.q, qo, 0, STATE_LOAD_POLICY);
+      L.q[r][0] = q4.x, L.q[r][1] = q4.y, L.q[r][2] = q4.z, L.q[r][3] = q4.w;
+    } else {
+      const u32x2_t q2 = __builtin_amdgcn_raw_buffer_load_b64(hb.q, qo >> 1, 0, STATE_LOAD_POLICY);
+      L.q[r][0] = q2.x, L.q[r][1] = q2.y, L.q[r][2] = 0, L.q[r][3] = 0;
+    }
+    if constexpr (Lay::mbits) {
+      L.m[r][0] = __builtin_amdgcn_raw_buffer_load_b8(hb.m, qo >> 4, 0, STATE_LOAD_POLICY);
+      L.m[r][1] = 0;
+    } else {
+      const u32x2_t m2 = __builtin_amdgcn_raw_buffer_load_b64(hb.m, qo >> 1, 0, STATE_LOAD_POLICY);
+      L.m[r][0] = m2.x, L.m[r][1] = m2.y;
+    }
     L.e[r] = __builtin_amdgcn_raw_buffer_load_b8(hb.e, qo >> 4, 0, STATE_LOAD_POLICY);
     L.xw[r] = __builtin_amdgcn_raw_buffer_load_b32(hb.x, (pc * p.x_row_bytes) & ~3u, 0, 0);
     L.zw[r] = __builtin_amdgcn_raw_buffer_load_b32(hb.z, (pc * p.z_row_bytes) & ~3u, 0, 0);
@@ -548,7 +652,7 @@ __device__ __forceinline__ void load_rows(const MxUpdateParams& p, const HeadBuf
 }
 
 // Update, y, and writeback encode of the R rows held in L.
-template <int FB, int RMODE, int BPR_LOG2, int R, int SLOTS>
+template <int FB, int RMODE, int BPR_LOG2, int R, int SLOTS, int LY>
 __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadBufs& hb, int b,
                                             int h, int row0, int slot, int blk,
                                             const RowLoads<R>& L, const float (&Bd)[16],
@@ -565,17 +669,14 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
     // h' = h * exp(A dt) + (B dt) x, with the decay folded into the two pair scales (exact)
     const float s0 = pin(__uint_as_float(L.e[r] << 23) * hs.dA);
     const float s1 = pin(__uint_as_float((L.e[r] + 1u) << 23) * hs.dA);
-    const uint32_t qa[4] = {L.q[r].x, L.q[r].y, L.q[r].z, L.q[r].w};
-    const uint32_t ma[2] = {L.m[r].x, L.m[r].y};
     float hv[16];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const float sk = ((ma[k >> 2] >> (8 * (k & 3))) & 0xffu) ? s1 : s0;
+      const float sk = micro<LY>(L.m[r], k) ? s1 : s0;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int n = 2 * k + i;
-        const float qv = (float)(int)(int8_t)(qa[n >> 2] >> (8 * (n & 3)));
-        hv[n] = fmaf(qv, sk, Bd[n] * xv);
+        hv[n] = fmaf(mant<LY>(L.q[r], n), sk, Bd[n] * xv);
       }
     }
     float ypart = 0.0f;
@@ -611,18 +712,28 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
         x *= 0x846ca68bu;
         pw[k] = x ^ (x >> 16);
       }
-      encode16_dither<FB>(hv, pw, qo, mo, eo);
+      encode16_dither<FB, LY>(hv, pw, qo, mo, eo);
     } else {
       float u16[16];
       block_u16<RMODE>(p.uni, b, h, (int)pc, (int)n0, u16);
-      encode16<FB, RMODE>(hv, u16, qo, mo, eo);
+      encode16<FB, RMODE, LY>(hv, u16, qo, mo, eo);
     }
     if (act) {
+      using Lay = LayoutOf<LY>;
       const uint32_t so = (uint32_t)pp * N + n0;
-      __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{qo[0], qo[1], qo[2], qo[3]}, hb.q, so, 0,
-                                             STATE_STORE_POLICY);
-      __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{mo[0], mo[1]}, hb.m, so >> 1, 0,
-                                            STATE_STORE_POLICY);
+      if constexpr (Lay::qbytes == 16) {
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{qo[0], qo[1], qo[2], qo[3]}, hb.q, so, 0,
+                                               STATE_STORE_POLICY);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{qo[0], qo[1]}, hb.q, so >> 1, 0,
+                                              STATE_STORE_POLICY);
+      }
+      if constexpr (Lay::mbits) {
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)mo[0], hb.m, so >> 4, 0, STATE_STORE_POLICY);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{mo[0], mo[1]}, hb.m, so >> 1, 0,
+                                              STATE_STORE_POLICY);
+      }
       __builtin_amdgcn_raw_buffer_store_b8((uint8_t)eo, hb.e, so >> 4, 0, STATE_STORE_POLICY);
     }
   }
@@ -630,7 +741,7 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
 
 // One work item per workgroup: grid (ceil(P / (R * SLOTS)), H, B). Every load of the lane (R state
 // blocks, x, B, C, the head scalars) is issued before the first use of any of them.
-template <int FB, int RMODE, int BPR_LOG2, int R, int THREADS>
+template <int FB, int RMODE, int BPR_LOG2, int R, int THREADS, int LY>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(LQ_MX_ROWS_WAVES)))
 void mx_update_rows_kernel(MxUpdateParams p) {
   constexpr int BPR = 1 << BPR_LOG2;
@@ -642,9 +753,9 @@ void mx_update_rows_kernel(MxUpdateParams p) {
   const uint32_t n0 = (uint32_t)blk * 16u;
   const int row0 = blockIdx.x * (R * SLOTS);
 
-  const HeadBufs hb = head_bufs<N>(p, b, h);
+  const HeadBufs hb = head_bufs<N, LY>(p, b, h);
   RowLoads<R> L;
-  load_rows<R, SLOTS, N>(p, hb, row0, slot, n0, L);
+  load_rows<R, SLOTS, N, LY>(p, hb, row0, slot, n0, L);
   u32x4_t bw[2], cw[2];
   load_bc(p, b, h / p.ratio, n0, N, bw, cw);
   const HeadScalars hs = head_scalars(p, b, h);
@@ -653,10 +764,10 @@ void mx_update_rows_kernel(MxUpdateParams p) {
   expand_bf16(cw, Cv);
 #pragma unroll
   for (int i = 0; i < 16; ++i) Bd[i] *= hs.dt;
-  update_rows<FB, RMODE, BPR_LOG2, R, SLOTS>(p, hb, b, h, row0, slot, blk, L, Bd, Cv, hs);
+  update_rows<FB, RMODE, BPR_LOG2, R, SLOTS, LY>(p, hb, b, h, row0, slot, blk, L, Bd, Cv, hs);
 }
 
-template <int FB, int RMODE, bool VEC>
+template <int FB, int RMODE, bool VEC, int LY>
 __global__ __launch_bounds__(256) void mx_encode_kernel(MxCodecParams p) {
   const LaneIdx L = lane_index(p.P, p.vbpr_log2, p.bpr);
   if (!L.active) return;
@@ -669,27 +780,27 @@ __global__ __launch_bounds__(256) void mx_encode_kernel(MxCodecParams p) {
   for (int i = 0; i < 16; ++i) v[i] = ldf(vb, p.v.dtype, voff + i * (int)p.v.s[3]);
   const uint64_t row = ((uint64_t)b * p.H + h) * p.P + pp;
   uint32_t qw[4], mw[2], eb;
-  encode_block<FB, RMODE>(v, p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0, b, h,
-                          pp, n0, qw, mw, eb);
-  int8_t* qp = p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1] + pp * (int)p.st.qs[2] + n0;
-  uint8_t* mp = p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1] + pp * (int)p.st.ms[2] + L.blk * 8;
-  uint8_t* ep = p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1] + pp * (int)p.st.es[2] + L.blk;
-  store_block<VEC>(qp, mp, ep, qw, mw, eb);
+  encode_block<FB, RMODE, LY>(v, p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0,
+                              b, h, pp, n0, qw, mw, eb);
+  int8_t* qp;
+  uint8_t *mp, *ep;
+  block_ptrs<LY>(p.st, b, h, pp, L.blk, qp, mp, ep);
+  store_block<VEC, LY>(qp, mp, ep, qw, mw, eb);
 }
 
-template <bool VEC>
+template <bool VEC, int LY>
 __global__ __launch_bounds__(256) void mx_decode_kernel(MxCodecParams p) {
   const LaneIdx L = lane_index(p.P, p.vbpr_log2, p.bpr);
   if (!L.active) return;
   const int b = L.b, h = L.h, pp = L.pp;
   const int n0 = L.blk * 16;
-  const int8_t* qp = p.st.q + (int64_t)b * p.st.qs[0] + (int64_t)h * p.st.qs[1] + pp * (int)p.st.qs[2] + n0;
-  const uint8_t* mp = p.st.mi + (int64_t)b * p.st.ms[0] + (int64_t)h * p.st.ms[1] + pp * (int)p.st.ms[2] + L.blk * 8;
-  const uint8_t* ep = p.st.e + (int64_t)b * p.st.es[0] + (int64_t)h * p.st.es[1] + pp * (int)p.st.es[2] + L.blk;
+  int8_t* qp;
+  uint8_t *mp, *ep;
+  block_ptrs<LY>(p.st, b, h, pp, L.blk, qp, mp, ep);
   uint32_t qw[4], mw[2], ev;
-  load_block<VEC>(qp, mp, ep, qw, mw, ev);
+  load_block<VEC, LY>(qp, mp, ep, qw, mw, ev);
   float hv[16];
-  decode16(qw, mw, ev, hv);
+  decode16<LY>(qw, mw, ev, hv);
   char* ob = (char*)vbase(p.v, b, h);
   const int off = pp * (int)p.v.s[2] + n0 * (int)p.v.s[3];
 #pragma unroll
@@ -720,30 +831,50 @@ static uint32_t seed_key(uint64_t seed) {
   return lowbias32_host((uint32_t)seed ^ lowbias32_host((uint32_t)(seed >> 32) ^ 0x9E3779B9u));
 }
 
+// Validates the three MX state tensors and finds their layout from the shapes: with
+// NB = shared_exp.shape[3] blocks per row (N = 16 NB values), q_state is [B,H,P,N] (one byte per
+// mantissa) or [B,H,P,N/2] (MX4 nibbles), micro_exp [B,H,P,N/2] (one byte per pair) or
+// [B,H,P,NB] (bits): reference = bytes + bytes, compact MX8 = bytes + bits, compact MX4 =
+// nibbles + bits. `vec`: q and micro blocks aligned for vector access.
 static int check_state(const lq_tensor* q, const lq_tensor* e, const lq_tensor* m, int64_t& Bn,
-                       int64_t& H, int64_t& P, int64_t& N, MxState& st, bool& vec) {
+                       int64_t& H, int64_t& P, int64_t& N, MxState& st, bool& vec, int& layout) {
   int rc;
-  if ((rc = check_tensor(q, "q_state", 4, false, LQ_I8)) != LQ_OK) return rc;
+  if ((rc = check_tensor(q, "q_state", 4, false)) != LQ_OK) return rc;
   if ((rc = check_tensor(e, "shared_exp", 4, false, LQ_U8)) != LQ_OK) return rc;
   if ((rc = check_tensor(m, "micro_exp", 4, false, LQ_U8)) != LQ_OK) return rc;
-  Bn = q->shape[0];
-  H = q->shape[1];
-  P = q->shape[2];
-  N = q->shape[3];
-  if (N % 16 != 0) {
-    return fail(LQ_ERR_INVALID_ARG, "MX state dim must be divisible by 16, got %lld", (long long)N);
-  }
+  Bn = e->shape[0];
+  H = e->shape[1];
+  P = e->shape[2];
+  N = 16 * e->shape[3];
   if (N / 16 > 64) {
     return fail(LQ_ERR_UNSUPPORTED, "MX state dim %lld exceeds 1024", (long long)N);
   }
-  const int64_t want_e[4] = {Bn, H, P, N / 16};
-  const int64_t want_m[4] = {Bn, H, P, N / 2};
-  for (int i = 0; i < 4; ++i) {
-    if (e->shape[i] != want_e[i]) {
-      return fail(LQ_ERR_INVALID_ARG, "shared_exp must be [B, H, P, N/16]");
+  const int64_t qn = q->shape[3];
+  const bool qnib = qn * 2 == N && N > 0;
+  if (qn != N && !qnib) {
+    if (qn % 16 != 0) {
+      return fail(LQ_ERR_INVALID_ARG, "MX state dim must be divisible by 16, got %lld", (long long)qn);
     }
-    if (m->shape[i] != want_m[i]) {
-      return fail(LQ_ERR_INVALID_ARG, "micro_exp must be [B, H, P, N/2]");
+    return fail(LQ_ERR_INVALID_ARG,
+                "q_state must be [B, H, P, N] or, MX4 nibbles, [B, H, P, N/2] (N = 16 * shared_exp dim)");
+  }
+  const bool mbits = m->shape[3] == N / 16;
+  if (!mbits && m->shape[3] != N / 2) {
+    return fail(LQ_ERR_INVALID_ARG, "micro_exp must be [B, H, P, N/2] or, bits, [B, H, P, N/16]");
+  }
+  if (qnib && !mbits) {
+    return fail(LQ_ERR_INVALID_ARG, "nibble mantissas need bit micro-exponents [B, H, P, N/16]");
+  }
+  layout = qnib ? LAYOUT_CM4 : (mbits ? LAYOUT_CM8 : LAYOUT_REF);
+  if (layout == LAYOUT_REF && q->dtype != LQ_I8) {
+    return fail(LQ_ERR_INVALID_ARG, "q_state: dtype code %d, expected %d", q->dtype, LQ_I8);
+  }
+  if (q->dtype != LQ_I8 && q->dtype != LQ_U8) {
+    return fail(LQ_ERR_INVALID_ARG, "q_state: dtype code %d, expected int8 or uint8", q->dtype);
+  }
+  for (int i = 0; i < 3; ++i) {
+    if (q->shape[i] != e->shape[i] || m->shape[i] != e->shape[i]) {
+      return fail(LQ_ERR_INVALID_ARG, "q_state, shared_exp and micro_exp must share [B, H, P]");
     }
   }
   if (q->stride[3] != 1 || e->stride[3] != 1 || m->stride[3] != 1) {
@@ -752,12 +883,14 @@ static int check_state(const lq_tensor* q, const lq_tensor* e, const lq_tensor* 
   st.q = (int8_t*)q->data;
   st.e = (uint8_t*)e->data;
   st.mi = (uint8_t*)m->data;
-  vec = (((uintptr_t)st.q & 15) == 0) && (((uintptr_t)st.mi & 7) == 0);
+  const int qa = qnib ? 8 : 16;
+  const int ma = mbits ? 1 : 8;
+  vec = (((uintptr_t)st.q % qa) == 0) && (((uintptr_t)st.mi % ma) == 0);
   for (int i = 0; i < 3; ++i) {
     st.qs[i] = q->stride[i];
     st.es[i] = e->stride[i];
     st.ms[i] = m->stride[i];
-    vec = vec && (st.qs[i] % 16 == 0) && (st.ms[i] % 8 == 0);
+    vec = vec && (st.qs[i] % qa == 0) && (st.ms[i] % ma == 0);
   }
   return LQ_OK;
 }
@@ -832,52 +965,70 @@ static bool bc_vector_ok(const lq_tensor* t) {
          t->stride[0] % 8 == 0 && t->stride[1] % 8 == 0;
 }
 
-template <int FB, int RMODE>
-static void launch_update(const MxUpdateParams& p, bool vec, bool bcvec, dim3 grid,
-                          hipStream_t st) {
-  if (vec && bcvec) {
-    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, true, true>), grid, dim3(256), 0, st, p);
-  } else if (vec) {
-    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, true, false>), grid, dim3(256), 0, st, p);
-  } else if (bcvec) {
-    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, false, true>), grid, dim3(256), 0, st, p);
-  } else {
-    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, false, false>), grid, dim3(256), 0, st, p);
+// Calls f(std::integral_constant<int, LY>) for the layout code (compact MX4 only with 4-bit
+// mantissas, which the nibbles can hold); returns an error for an impossible combination.
+template <int FB, class F>
+static int with_layout(int layout, F&& f) {
+  switch (layout) {
+    case LAYOUT_REF: f(std::integral_constant<int, LAYOUT_REF>{}); return LQ_OK;
+    case LAYOUT_CM8: f(std::integral_constant<int, LAYOUT_CM8>{}); return LQ_OK;
+    default:
+      if constexpr (FB == 4) {
+        f(std::integral_constant<int, LAYOUT_CM4>{});
+        return LQ_OK;
+      } else {
+        return fail(LQ_ERR_INVALID_ARG,
+                    "nibble mantissas hold MX4 only (format_bits=8 needs [B, H, P, N] q_state)");
+      }
   }
 }
 
-template <int FB>
+template <int FB, int RMODE, int LY>
+static void launch_update(const MxUpdateParams& p, bool vec, bool bcvec, dim3 grid,
+                          hipStream_t st) {
+  if (vec && bcvec) {
+    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, true, true, LY>), grid, dim3(256), 0, st, p);
+  } else if (vec) {
+    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, true, false, LY>), grid, dim3(256), 0, st, p);
+  } else if (bcvec) {
+    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, false, true, LY>), grid, dim3(256), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((mx_update_kernel<FB, RMODE, false, false, LY>), grid, dim3(256), 0, st, p);
+  }
+}
+
+template <int FB, int LY>
 static void dispatch_update(const MxUpdateParams& p, int rmode, bool vec, bool bcvec, dim3 grid,
                             hipStream_t st) {
   switch (rmode) {
     case LQ_ROUND_NEAREST_EVEN:
-      launch_update<FB, LQ_ROUND_NEAREST_EVEN>(p, vec, bcvec, grid, st);
+      launch_update<FB, LQ_ROUND_NEAREST_EVEN, LY>(p, vec, bcvec, grid, st);
       break;
-    case LQ_ROUND_HALF_UP: launch_update<FB, LQ_ROUND_HALF_UP>(p, vec, bcvec, grid, st); break;
+    case LQ_ROUND_HALF_UP: launch_update<FB, LQ_ROUND_HALF_UP, LY>(p, vec, bcvec, grid, st); break;
     case LQ_ROUND_SR_UNIFORM:
-      launch_update<FB, LQ_ROUND_SR_UNIFORM>(p, vec, bcvec, grid, st);
+      launch_update<FB, LQ_ROUND_SR_UNIFORM, LY>(p, vec, bcvec, grid, st);
       break;
-    default: launch_update<FB, LQ_ROUND_SR_COUNTER>(p, vec, bcvec, grid, st); break;
+    default: launch_update<FB, LQ_ROUND_SR_COUNTER, LY>(p, vec, bcvec, grid, st); break;
   }
 }
 
-template <int FB, int RMODE>
+template <int FB, int RMODE, int LY>
 static void launch_encode(const MxCodecParams& p, bool vec, dim3 grid, hipStream_t st) {
   if (vec) {
-    hipLaunchKernelGGL((mx_encode_kernel<FB, RMODE, true>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((mx_encode_kernel<FB, RMODE, true, LY>), grid, dim3(256), 0, st, p);
   } else {
-    hipLaunchKernelGGL((mx_encode_kernel<FB, RMODE, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((mx_encode_kernel<FB, RMODE, false, LY>), grid, dim3(256), 0, st, p);
   }
 }
 
-template <int FB>
+template <int FB, int LY>
 static void dispatch_encode(const MxCodecParams& p, int rmode, bool vec, dim3 grid,
                             hipStream_t st) {
   switch (rmode) {
-    case LQ_ROUND_NEAREST_EVEN: launch_encode<FB, LQ_ROUND_NEAREST_EVEN>(p, vec, grid, st); break;
-    case LQ_ROUND_HALF_UP: launch_encode<FB, LQ_ROUND_HALF_UP>(p, vec, grid, st); break;
-    case LQ_ROUND_SR_UNIFORM: launch_encode<FB, LQ_ROUND_SR_UNIFORM>(p, vec, grid, st); break;
-    default: launch_encode<FB, LQ_ROUND_SR_COUNTER>(p, vec, grid, st); break;
+    case LQ_ROUND_NEAREST_EVEN: launch_encode<FB, LQ_ROUND_NEAREST_EVEN, LY>(p, vec, grid, st); break;
+    case LQ_ROUND_HALF_UP: launch_encode<FB, LQ_ROUND_HALF_UP, LY>(p, vec, grid, st); break;
+    case LQ_ROUND_SR_UNIFORM: launch_encode<FB, LQ_ROUND_SR_UNIFORM, LY>(p, vec, grid, st); break;
+    default: launch_encode<FB, LQ_ROUND_SR_COUNTER, LY>(p, vec, grid, st); break;
   }
 }
 
@@ -892,36 +1043,36 @@ static void dispatch_encode(const MxCodecParams& p, int rmode, bool vec, dim3 gr
 constexpr int ROWS_R = LQ_MX_ROWS_R;
 constexpr int ROWS_THREADS = LQ_MX_ROWS_THREADS;
 
-template <int FB, int BPR_LOG2>
+template <int FB, int BPR_LOG2, int LY>
 static void launch_rows(const MxUpdateParams& p, int rmode, dim3 grid, hipStream_t st) {
   constexpr int R = ROWS_R, T = ROWS_THREADS;
   const dim3 block(T);
   switch (rmode) {
     case LQ_ROUND_NEAREST_EVEN:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_NEAREST_EVEN, BPR_LOG2, R, T>), grid,
-                         block, 0, st, p);
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_NEAREST_EVEN, BPR_LOG2, R, T, LY>),
+                         grid, block, 0, st, p);
       break;
     case LQ_ROUND_HALF_UP:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_HALF_UP, BPR_LOG2, R, T>), grid,
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_HALF_UP, BPR_LOG2, R, T, LY>), grid,
                          block, 0, st, p);
       break;
     case LQ_ROUND_SR_UNIFORM:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_UNIFORM, BPR_LOG2, R, T>), grid,
-                         block, 0, st, p);
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_UNIFORM, BPR_LOG2, R, T, LY>),
+                         grid, block, 0, st, p);
       break;
     default:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_COUNTER, BPR_LOG2, R, T>), grid,
-                         block, 0, st, p);
+      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_COUNTER, BPR_LOG2, R, T, LY>),
+                         grid, block, 0, st, p);
       break;
   }
 }
 
-template <int FB>
+template <int FB, int LY>
 static void dispatch_rows(const MxUpdateParams& p, int rmode, dim3 grid, hipStream_t st) {
   switch (p.vbpr_log2) {
-    case 2: launch_rows<FB, 2>(p, rmode, grid, st); break;
-    case 3: launch_rows<FB, 3>(p, rmode, grid, st); break;
-    default: launch_rows<FB, 4>(p, rmode, grid, st); break;
+    case 2: launch_rows<FB, 2, LY>(p, rmode, grid, st); break;
+    case 3: launch_rows<FB, 3, LY>(p, rmode, grid, st); break;
+    default: launch_rows<FB, 4, LY>(p, rmode, grid, st); break;
   }
 }
 
@@ -931,12 +1082,14 @@ static void dispatch_rows(const MxUpdateParams& p, int rmode, dim3 grid, hipStre
 // of the launch sharing one high word, with fewer than 2^32 state elements.
 static bool rows_path_ok(const MxUpdateParams& p, bool vec, bool bcvec, const lq_tensor* dt,
                          const lq_tensor* dt_bias, const lq_tensor* A, const lq_tensor* D,
-                         int round_mode, int64_t total) {
+                         int round_mode, int64_t total, int layout) {
   const char* force = getenv("LQ_MX_FORCE_GENERIC");
   if (force != nullptr && force[0] != '\0' && force[0] != '0') return false;
   if (!vec || !bcvec) return false;
   if (p.N != 64 && p.N != 128 && p.N != 256) return false;
-  if (p.st.qs[2] != p.N || p.st.ms[2] != p.N / 2 || p.st.es[2] != p.N / 16) return false;
+  const int64_t q_row = layout == LAYOUT_CM4 ? p.N / 2 : p.N;
+  const int64_t m_row = layout == LAYOUT_REF ? p.N / 2 : p.N / 16;
+  if (p.st.qs[2] != q_row || p.st.ms[2] != m_row || p.st.es[2] != p.N / 16) return false;
   if (dt->stride[2] != 0 || A->stride[1] != 0 || A->stride[2] != 0) return false;
   // byte offsets of x, z and out rows within a (batch, head) slice are 32-bit
   const int64_t lim = (int64_t)1 << 28;
@@ -982,7 +1135,10 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
   int64_t Bn, H, P, N;
   MxState st{};
   bool vec = false;
-  if ((rc = check_state(q_state, shared_exp, micro_exp, Bn, H, P, N, st, vec)) != LQ_OK) return rc;
+  int layout = LAYOUT_REF;
+  if ((rc = check_state(q_state, shared_exp, micro_exp, Bn, H, P, N, st, vec, layout)) != LQ_OK) {
+    return rc;
+  }
   if ((rc = check_shape3(x, "x", Bn, H, P, false)) != LQ_OK) return rc;
   if (B == nullptr || C == nullptr || B->ndim != 3 || C->ndim != 3) {
     return fail(LQ_ERR_INVALID_ARG,
@@ -1053,7 +1209,11 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
   if ((rc = grid_for(Bn, H, P, p.vbpr_log2, grid)) != LQ_OK) return rc;
   const bool bcvec = bc_vector_ok(B) && bc_vector_ok(C);
   hipStream_t s = (hipStream_t)stream;
-  if (rows_path_ok(p, vec, bcvec, dt, dt_bias, A, D, round_mode, Bn * H * P * N)) {
+  if (layout == LAYOUT_CM4 && format_bits != 4) {
+    return fail(LQ_ERR_INVALID_ARG,
+                "nibble mantissas hold MX4 only (format_bits=8 needs [B, H, P, N] q_state)");
+  }
+  if (rows_path_ok(p, vec, bcvec, dt, dt_bias, A, D, round_mode, Bn * H * P * N, layout)) {
     p.lo_base = (uint32_t)(rng_offset >> 1);
     p.kh = lowbias32_host((uint32_t)(rng_offset >> 33) ^ p.key);
     // per-row byte strides and slice spans of x, z and out
@@ -1080,17 +1240,21 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
     const int rows = ROWS_R * (ROWS_THREADS >> p.vbpr_log2);
     const dim3 rgrid((unsigned)((P + rows - 1) / rows), (unsigned)H, (unsigned)Bn);
     if (format_bits == 8) {
-      dispatch_rows<8>(p, round_mode, rgrid, s);
+      rc = with_layout<8>(layout, [&](auto ly) { dispatch_rows<8, ly()>(p, round_mode, rgrid, s); });
     } else {
-      dispatch_rows<4>(p, round_mode, rgrid, s);
+      rc = with_layout<4>(layout, [&](auto ly) { dispatch_rows<4, ly()>(p, round_mode, rgrid, s); });
     }
+    if (rc != LQ_OK) return rc;
     return check_launch("lq_mx_state_update");
   }
   if (format_bits == 8) {
-    dispatch_update<8>(p, round_mode, vec, bcvec, grid, s);
+    rc = with_layout<8>(layout,
+                        [&](auto ly) { dispatch_update<8, ly()>(p, round_mode, vec, bcvec, grid, s); });
   } else {
-    dispatch_update<4>(p, round_mode, vec, bcvec, grid, s);
+    rc = with_layout<4>(layout,
+                        [&](auto ly) { dispatch_update<4, ly()>(p, round_mode, vec, bcvec, grid, s); });
   }
+  if (rc != LQ_OK) return rc;
   return check_launch("lq_mx_state_update");
 }
 
@@ -1102,7 +1266,10 @@ extern "C" int lq_mx_encode(const lq_tensor* state, const lq_tensor* q_state,
   int64_t Bn, H, P, N;
   MxState st{};
   bool vec = false;
-  if ((rc = check_state(q_state, shared_exp, micro_exp, Bn, H, P, N, st, vec)) != LQ_OK) return rc;
+  int layout = LAYOUT_REF;
+  if ((rc = check_state(q_state, shared_exp, micro_exp, Bn, H, P, N, st, vec, layout)) != LQ_OK) {
+    return rc;
+  }
   if ((rc = check_tensor(state, "state", 4, true)) != LQ_OK) return rc;
   for (int i = 0; i < 4; ++i) {
     const int64_t want[4] = {Bn, H, P, N};
@@ -1133,11 +1300,16 @@ extern "C" int lq_mx_encode(const lq_tensor* state, const lq_tensor* q_state,
   dim3 grid;
   if ((rc = grid_for(Bn, H, P, p.vbpr_log2, grid)) != LQ_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
-  if (format_bits == 8) {
-    dispatch_encode<8>(p, round_mode, vec, grid, s);
-  } else {
-    dispatch_encode<4>(p, round_mode, vec, grid, s);
+  if (layout == LAYOUT_CM4 && format_bits != 4) {
+    return fail(LQ_ERR_INVALID_ARG,
+                "nibble mantissas hold MX4 only (format_bits=8 needs [B, H, P, N] q_state)");
   }
+  if (format_bits == 8) {
+    rc = with_layout<8>(layout, [&](auto ly) { dispatch_encode<8, ly()>(p, round_mode, vec, grid, s); });
+  } else {
+    rc = with_layout<4>(layout, [&](auto ly) { dispatch_encode<4, ly()>(p, round_mode, vec, grid, s); });
+  }
+  if (rc != LQ_OK) return rc;
   return check_launch("lq_mx_encode");
 }
 
@@ -1147,7 +1319,10 @@ extern "C" int lq_mx_decode(const lq_tensor* q_state, const lq_tensor* shared_ex
   int64_t Bn, H, P, N;
   MxState st{};
   bool vec = false;
-  if ((rc = check_state(q_state, shared_exp, micro_exp, Bn, H, P, N, st, vec)) != LQ_OK) return rc;
+  int layout = LAYOUT_REF;
+  if ((rc = check_state(q_state, shared_exp, micro_exp, Bn, H, P, N, st, vec, layout)) != LQ_OK) {
+    return rc;
+  }
   if ((rc = check_tensor(out, "out", 4, true)) != LQ_OK) return rc;
   for (int i = 0; i < 4; ++i) {
     const int64_t want[4] = {Bn, H, P, N};
@@ -1171,10 +1346,13 @@ extern "C" int lq_mx_decode(const lq_tensor* q_state, const lq_tensor* shared_ex
   }
   dim3 grid;
   if ((rc = grid_for(Bn, H, P, p.vbpr_log2, grid)) != LQ_OK) return rc;
-  if (vec) {
-    hipLaunchKernelGGL(mx_decode_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, p);
-  } else {
-    hipLaunchKernelGGL(mx_decode_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, p);
-  }
+  rc = with_layout<4>(layout, [&](auto ly) {
+    if (vec) {
+      hipLaunchKernelGGL((mx_decode_kernel<true, ly()>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    } else {
+      hipLaunchKernelGGL((mx_decode_kernel<false, ly()>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    }
+  });
+  if (rc != LQ_OK) return rc;
   return check_launch("lq_mx_decode");
 }

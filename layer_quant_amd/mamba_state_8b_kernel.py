@@ -49,17 +49,42 @@ class MambaStateKernelCache:
     micro_exp: torch.Tensor
     format_bits: int = 8
     step: int = 0
+    layout: str = "reference"
+
+    @property
+    def state_shape(self) -> tuple[int, ...]:
+        """[B, H, P, N] of the state this cache holds (N = 16 * the exponent dimension)."""
+        return (*self.shared_exp.shape[:-1], self.shared_exp.shape[-1] * MX8_BLOCK_SIZE)
 
 
-def _empty_mx_tensors(shape, device):
+# State layouts. "reference": q_state int8 [..., N] (one byte per mantissa, both formats),
+# micro_exp uint8 [..., N/2] (one byte per pair) -- the reference's, interchangeable with it.
+# "compact" (no reference counterpart): micro_exp uint8 [..., N/16] with bit k of byte j the
+# micro-exponent of pair 8j + k; MX4 q_state uint8 [..., N/2] with two two's-complement nibbles
+# per byte (value 2p low, 2p + 1 high); MX8 q_state as in the reference. shared_exp is the same.
+# Same arithmetic and bit-identical states in either layout; compact MX4 moves 80 bytes per
+# 128-value row instead of 200.
+STATE_LAYOUTS = ("reference", "compact")
+
+
+def _empty_mx_tensors(shape, device, format_bits: int = 8, layout: str = "reference"):
     *lead, n = shape
-    return (torch.empty(shape, dtype=torch.int8, device=device),
-            torch.empty((*lead, n // MX8_BLOCK_SIZE), dtype=torch.uint8, device=device),
-            torch.empty((*lead, n // MX8_PAIR_SIZE), dtype=torch.uint8, device=device))
+    if layout not in STATE_LAYOUTS:
+        raise ValueError(f"Unknown MX state layout {layout!r}; expected one of {STATE_LAYOUTS}")
+    if layout == "compact":
+        if format_bits == 4:
+            q = torch.empty((*lead, n // 2), dtype=torch.uint8, device=device)
+        else:
+            q = torch.empty(shape, dtype=torch.int8, device=device)
+        m = torch.empty((*lead, n // MX8_BLOCK_SIZE), dtype=torch.uint8, device=device)
+    else:
+        q = torch.empty(shape, dtype=torch.int8, device=device)
+        m = torch.empty((*lead, n // MX8_PAIR_SIZE), dtype=torch.uint8, device=device)
+    return q, torch.empty((*lead, n // MX8_BLOCK_SIZE), dtype=torch.uint8, device=device), m
 
 
 def _quantize_initial_state_mx(state: torch.Tensor, *, format_bits: int, block_size: int,
-                               pair_size: int, mantissa_max: float):
+                               pair_size: int, mantissa_max: float, layout: str = "reference"):
     """Nearest-even MX encode of a float state [..., N] (ms.py:547-572).
 
     Runs lq_mx_encode on the state's GPU. The block and pair sizes and the mantissa maximum are
@@ -76,32 +101,35 @@ def _quantize_initial_state_mx(state: torch.Tensor, *, format_bits: int, block_s
             f"pair_size={pair_size}, mantissa_max={mantissa_max}")
     lead = state.shape[:-1]
     state4 = state.reshape(-1, 1, 1, state.shape[-1]) if state.dim() != 4 else state
-    q, e, m = _empty_mx_tensors(tuple(state4.shape), state.device)
+    q, e, m = _empty_mx_tensors(tuple(state4.shape), state.device, format_bits, layout)
     _abi.mx_encode(state4, q, e, m, format_bits, _abi.ROUND_NEAREST_EVEN)
-    n = state.shape[-1]
-    return (q.reshape(*lead, n), e.reshape(*lead, n // block_size),
-            m.reshape(*lead, n // pair_size))
+    return (q.reshape(*lead, q.shape[-1]), e.reshape(*lead, e.shape[-1]),
+            m.reshape(*lead, m.shape[-1]))
 
 
 def allocate_state_kernel_cache(ssm_state_4d: torch.Tensor, group_size: int = MX8_BLOCK_SIZE,
-                                format_bits: int = 8) -> MambaStateKernelCache:
-    """Encode a layer's state [B,H,P,N] into a new MX cache (ms.py:575-598)."""
+                                format_bits: int = 8, *,
+                                layout: str = "reference") -> MambaStateKernelCache:
+    """Encode a layer's state [B,H,P,N] into a new MX cache (ms.py:575-598); `layout` selects the
+    reference's tensors (default) or the compact ones (see STATE_LAYOUTS)."""
     if format_bits == 8:
         if group_size != MX8_BLOCK_SIZE:
             raise ValueError(
                 f"MX8 uses a fixed {MX8_BLOCK_SIZE}-value block, got group_size={group_size}")
         q, e, m = _quantize_initial_state_mx(ssm_state_4d, format_bits=8,
                                              block_size=MX8_BLOCK_SIZE, pair_size=MX8_PAIR_SIZE,
-                                             mantissa_max=MX8_MANTISSA_MAX)
-        return MambaStateKernelCache(q_state=q, shared_exp=e, micro_exp=m, format_bits=8)
+                                             mantissa_max=MX8_MANTISSA_MAX, layout=layout)
+        return MambaStateKernelCache(q_state=q, shared_exp=e, micro_exp=m, format_bits=8,
+                                     layout=layout)
     if format_bits == 4:
         if group_size != MX4_BLOCK_SIZE:
             raise ValueError(
                 f"MX4 uses a fixed {MX4_BLOCK_SIZE}-value block, got group_size={group_size}")
         q, e, m = _quantize_initial_state_mx(ssm_state_4d, format_bits=4,
                                              block_size=MX4_BLOCK_SIZE, pair_size=MX4_PAIR_SIZE,
-                                             mantissa_max=MX4_MANTISSA_MAX)
-        return MambaStateKernelCache(q_state=q, shared_exp=e, micro_exp=m, format_bits=4)
+                                             mantissa_max=MX4_MANTISSA_MAX, layout=layout)
+        return MambaStateKernelCache(q_state=q, shared_exp=e, micro_exp=m, format_bits=4,
+                                     layout=layout)
     raise ValueError(
         f"Only MX8 and MX4 state quantization are supported, got format_bits={format_bits}")
 
@@ -110,8 +138,40 @@ def dequantize_state_cache(cache: MambaStateKernelCache,
                            dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """Decoded state q * 2^(e - 127 + micro) [B,H,P,N] (no reference counterpart; the
     reference decodes only inside its update kernels, ms.py:132, 322)."""
-    out = torch.empty(cache.q_state.shape, dtype=dtype, device=cache.q_state.device)
+    out = torch.empty(cache.state_shape, dtype=dtype, device=cache.q_state.device)
     return _abi.mx_decode(cache.q_state, cache.shared_exp, cache.micro_exp, out)
+
+
+def convert_state_cache_layout(cache: MambaStateKernelCache, layout: str) -> MambaStateKernelCache:
+    """The same MX state in the other layout (bit-exact, lossless; the step counter is kept).
+    No reference counterpart: the compact layout is this build's."""
+    if layout not in STATE_LAYOUTS:
+        raise ValueError(f"Unknown MX state layout {layout!r}; expected one of {STATE_LAYOUTS}")
+    if layout == cache.layout:
+        return cache
+    q, e, m = cache.q_state, cache.shared_exp, cache.micro_exp
+    *lead, n = cache.state_shape
+    shifts = torch.arange(8, device=m.device, dtype=torch.int32)
+    if layout == "compact":
+        if cache.format_bits == 4:
+            u = q.view(torch.uint8).to(torch.int32) & 0x0F
+            q2 = (u[..., 0::2] | (u[..., 1::2] << 4)).to(torch.uint8)
+        else:
+            q2 = q.clone()
+        bits = m.reshape(*lead, n // MX8_BLOCK_SIZE, 8).to(torch.int32) & 1
+        m2 = (bits << shifts).sum(dim=-1).to(torch.uint8)
+    else:
+        if cache.format_bits == 4:
+            u = q.to(torch.int32)
+            lo, hi = u & 0x0F, (u >> 4) & 0x0F
+            q2 = torch.stack((lo, hi), dim=-1).reshape(*lead, n)
+            q2 = torch.where(q2 > 7, q2 - 16, q2).to(torch.int8)
+        else:
+            q2 = q.clone()
+        m2 = ((m.to(torch.int32)[..., None] >> shifts) & 1).reshape(*lead, n // 2).to(torch.uint8)
+    return MambaStateKernelCache(q_state=q2.contiguous(), shared_exp=e.clone(),
+                                 micro_exp=m2.contiguous(), format_bits=cache.format_bits,
+                                 step=cache.step, layout=layout)
 
 
 def _dt_bias_as_read(dt_bias: torch.Tensor | None, D: torch.Tensor | None, nheads: int,
@@ -148,7 +208,7 @@ def mx_state_selective_update(cache: MambaStateKernelCache, x: torch.Tensor, dt:
     """
     if cache.q_state.ndim != 4:
         raise ValueError(f"Expected q_state [B,H,P,N], got {tuple(cache.q_state.shape)}")
-    batch, nheads, dim, dstate = cache.q_state.shape
+    batch, nheads, dim, dstate = cache.state_shape
     if x.shape != (batch, nheads, dim):
         raise ValueError(f"Expected x shape {(batch, nheads, dim)}, got {tuple(x.shape)}")
     if B.ndim != 3 or C.ndim != 3:
@@ -251,9 +311,11 @@ def patch_nemotron_h_mamba_decode_state_kernel(model, group_size: int = MX8_BLOC
     model._mx_state_kernel_group_size = group_size
 
 
-def register_mamba_state_kernel_caches(model, cache_params, mode_by_layer: dict[int, str]) -> None:
+def register_mamba_state_kernel_caches(model, cache_params, mode_by_layer: dict[int, str], *,
+                                       layout: str = "reference") -> None:
     """Encode each listed layer's ssm_state into an MX cache keyed by id(ssm_state)
-    (ms.py:770-796); publishes the registry on the model and on the remote module."""
+    (ms.py:770-796); publishes the registry on the model and on the remote module. `layout`
+    (keyword only, no reference counterpart) selects the compact cache layout."""
     registry = {}
     for layer_idx, mode in mode_by_layer.items():
         if mode not in {"mx8", "mx4"}:
@@ -265,7 +327,7 @@ def register_mamba_state_kernel_caches(model, cache_params, mode_by_layer: dict[
         bits = 8 if mode == "mx8" else 4
         registry[id(ssm_state)] = allocate_state_kernel_cache(
             state_4d, group_size=MX8_BLOCK_SIZE if bits == 8 else MX4_BLOCK_SIZE,
-            format_bits=bits)
+            format_bits=bits, layout=layout)
     model._mamba_decode_state_kernel_caches = registry
     module = __import__(model.__class__.__module__, fromlist=["selective_state_update"])
     module._mamba_decode_state_kernel_caches = dict(registry)

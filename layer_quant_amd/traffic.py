@@ -21,13 +21,22 @@ def pack_bytes(batch: int, n_kv_heads: int, n_tokens: int, head_dim: int, group_
                                             + 4 * (head_dim // group_size))
 
 
+def mx_state_bytes(elems: int, format_bits: int = 8, layout: str = "reference") -> int:
+    """Bytes of an MX state of `elems` values: one exponent byte per 16 values, plus one byte per
+    mantissa and one per pair (reference layout), or nibble mantissas for MX4 and one micro bit per
+    pair (compact layout)."""
+    if layout == "compact":
+        return (elems // 2 if format_bits == 4 else elems) + elems // 16 + elems // 16
+    return elems + elems // 16 + elems // 2
+
+
 def mx_update_bytes(batch: int, nheads: int, dim: int, dstate: int, ngroups: int,
-                    x_bytes: int = 2, out_bytes: int = 2, dt_bytes: int = 2) -> int:
-    """One MX8/MX4 state update in the reference layout: the state (one byte per mantissa, one
-    exponent byte per 16 values, one micro-exponent byte per pair) read and written once, x and
-    y per row, B and C per group, dt per (batch, head), A, D and dt_bias per head."""
+                    x_bytes: int = 2, out_bytes: int = 2, dt_bytes: int = 2,
+                    format_bits: int = 8, layout: str = "reference") -> int:
+    """One MX8/MX4 state update: the state read and written once (mx_state_bytes), x and y per
+    row, B and C per group, dt per (batch, head), A, D and dt_bias per head."""
     elems = batch * nheads * dim * dstate
-    state = 2 * (elems + elems // 16 + elems // 2)
+    state = 2 * mx_state_bytes(elems, format_bits, layout)
     io = batch * nheads * dim * (x_bytes + out_bytes)
     bc = 2 * batch * ngroups * dstate * 2
     scalars = batch * nheads * dt_bytes + 3 * nheads * 4

@@ -37,8 +37,13 @@ for both signs, exact fractions) and its clamp;
 the update's closed forms (dt = 0 leaves h unchanged so the writeback is a pure re-encode;
 A = 0 gives h + dt*B*x; softplus threshold at 20) against an independent float64 evaluation.
 bf16_state_update (drift baseline) restates mamba_ssm's selective_state_update, a dependency
-(mamba-ssm 2.3.2.post1) that is not installed: parity unpinned beyond the HF torch fallback it
-follows (transformers nemotron_h mamba2_selective_state_update).
+(mamba-ssm 2.3.2.post1) that is not installed: its arithmetic is update_math (pinned above); bit
+parity with mamba-ssm's Triton kernel is unpinned.
+
+Compact layout (this build's opt-in cache layout, no reference counterpart): to_compact /
+from_compact convert the reference layout to micro-exponent bits (bit k of byte j = pair 8j + k
+of the row) and, for MX4, two's-complement nibble mantissas (byte p = value 2p in the low
+nibble, 2p + 1 in the high); pinned by a per-element loop over the bit layout and round trips.
 """
 from __future__ import annotations
 
@@ -164,6 +169,43 @@ def mx_decode(q, shared_exp, micro_exp) -> np.ndarray:
     scale = exp2_scale(e_full + m_full)
     assert scale.shape[-1] == n
     return (q.astype(np.float32) * scale).astype(np.float32)
+
+
+def to_compact(q: np.ndarray, shared_exp: np.ndarray, micro_exp: np.ndarray, format_bits: int):
+    """Reference layout -> compact layout (q nibbles for MX4, micro bits)."""
+    q = np.asarray(q, dtype=np.int8)
+    m = np.asarray(micro_exp, dtype=np.uint8)
+    *lead, n = q.shape
+    if format_bits == 4:
+        if np.abs(q.astype(np.int16)).max(initial=0) > 7:
+            raise ValueError("MX4 mantissas must lie in [-7, 7]")
+        u = q.view(np.uint8) & np.uint8(0x0F)
+        qc = (u[..., 0::2] | (u[..., 1::2] << np.uint8(4))).astype(np.uint8)
+    else:
+        qc = q.copy()
+    bits = m.reshape(*lead, n // BLOCK, 8).astype(np.uint32) & np.uint32(1)
+    mc = (bits << np.arange(8, dtype=np.uint32)).sum(axis=-1).astype(np.uint8)
+    return qc, np.asarray(shared_exp, dtype=np.uint8).copy(), mc
+
+
+def from_compact(qc: np.ndarray, shared_exp: np.ndarray, mc: np.ndarray, format_bits: int):
+    """Compact layout -> reference layout."""
+    qc = np.asarray(qc)
+    mc = np.asarray(mc, dtype=np.uint8)
+    *lead, nb = mc.shape
+    n = nb * BLOCK
+    if format_bits == 4:
+        u = qc.view(np.uint8) if qc.dtype == np.int8 else qc.astype(np.uint8)
+        lo = (u & np.uint8(0x0F)).astype(np.int16)
+        hi = (u >> np.uint8(4)).astype(np.int16)
+        q = np.empty((*lead, n), dtype=np.int16)
+        q[..., 0::2] = np.where(lo > 7, lo - 16, lo)
+        q[..., 1::2] = np.where(hi > 7, hi - 16, hi)
+        q = q.astype(np.int8)
+    else:
+        q = qc.astype(np.int8)
+    m = ((mc[..., None].astype(np.uint32) >> np.arange(8, dtype=np.uint32)) & np.uint32(1))
+    return q, np.asarray(shared_exp, dtype=np.uint8).copy(), m.reshape(*lead, n // PAIR).astype(np.uint8)
 
 
 def softplus_ref(x: torch.Tensor) -> torch.Tensor:

@@ -290,3 +290,32 @@ def test_package_byte_counts_match_the_oracle():
     # the unquantized update moves 2 bytes per state element each way
     assert traffic.ssm_update_bytes(64, 128, 64, 128, 8) - traffic.mx_update_bytes(64, 128, 64, 128, 8) \
         == 2 * 64 * 128 * 64 * 128 * (2 - (1 + 1 / 16 + 1 / 2))
+
+
+def test_compact_layout_bit_positions_and_round_trip():
+    """to_compact against a per-element loop over the documented bit layout (nibble of value n
+    at bits 4*(n%2) of byte n//2; micro bit of pair k at bit k%8 of byte k//8), and exact round
+    trips for encoded MX4 and MX8 states."""
+    rs = np.random.default_rng(3)
+    for fb in (4, 8):
+        h = (rs.standard_normal((2, 3, 5, 64)) * 0.5).astype(np.float32)
+        q, e, m = mx.mx_encode(h, fb, mx.ROUND_NEAREST_EVEN)
+        qc, ec, mc = mx.to_compact(q, e, m, fb)
+        assert np.array_equal(ec, e)
+        for idx in np.ndindex(*q.shape[:3]):
+            row_q, row_m = q[idx], m[idx]
+            for n in range(64):
+                if fb == 4:
+                    nib = (int(qc[idx][n // 2]) >> (4 * (n % 2))) & 0xF
+                    assert (nib - 16 if nib > 7 else nib) == int(row_q[n])
+                else:
+                    assert int(qc[idx][n]) == int(row_q[n])
+            for k in range(32):
+                assert ((int(mc[idx][k // 8]) >> (k % 8)) & 1) == int(row_m[k])
+        q2, e2, m2 = mx.from_compact(qc, ec, mc, fb)
+        assert np.array_equal(q2, q) and np.array_equal(e2, e) and np.array_equal(m2, m)
+        assert qc.shape[-1] == (32 if fb == 4 else 64) and mc.shape[-1] == 4
+        assert np.array_equal(mx.mx_decode(q2, e2, m2), mx.mx_decode(q, e, m))
+    with pytest.raises(ValueError):
+        mx.to_compact(np.full((1, 1, 1, 16), 9, np.int8), np.zeros((1, 1, 1, 1), np.uint8),
+                      np.zeros((1, 1, 1, 8), np.uint8), 4)
