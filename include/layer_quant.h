@@ -122,9 +122,19 @@ int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
                              void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * MX block encode of a float state [B, H, P, N] (N % 16 == 0) into the reference's MX layout:
- *   q_state [B,H,P,N] i8 (one byte per mantissa, also for MX4), shared_exp [B,H,P,N/16] u8
- *   (biased, 127 = 2^0), micro_exp [B,H,P,N/2] u8 (0/1 per pair).
+ * MX state layouts. Every MX entry point takes either layout and tells them apart by the shapes
+ * of q_state and micro_exp (N = 16 * shared_exp.shape[3]):
+ *   reference layout (hybrid_quant/mamba_state_8b_kernel.py:11-25, 575-598):
+ *     q_state [B,H,P,N] i8 (one byte per mantissa, also for MX4), shared_exp [B,H,P,N/16] u8
+ *     (biased, 127 = 2^0), micro_exp [B,H,P,N/2] u8 (0/1 per pair);
+ *   compact layout (no reference counterpart; same values, 2.5x (MX4) or 1.4x (MX8) fewer bytes):
+ *     q_state [B,H,P,N] i8 for MX8, or [B,H,P,N/2] u8 for MX4 with element 2j in the low nibble
+ *     of byte j and 2j+1 in the high (two's complement); shared_exp as above; micro_exp
+ *     [B,H,P,N/16] u8 with bit k of byte b = the micro-exponent of pair k of block b.
+ *   Nibble mantissas hold MX4 only (LQ_ERR_INVALID_ARG otherwise). Results are bit-identical in
+ *   both layouts.
+ *
+ * MX block encode of a float state [B, H, P, N] (N % 16 == 0) into either layout.
  * format_bits 8 -> mantissa max 63, 4 -> 7. With LQ_ROUND_NEAREST_EVEN this replaces
  * _quantize_initial_state_mx (reference hybrid_quant/mamba_state_8b_kernel.py:547-572); the
  * other modes run the writeback encoder of :168-222 / :494-544 on a given state.
