@@ -29,6 +29,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = ("µs/decode-step & achieved HBM GB/s (frac of 8 TB/s): INT4 attn, MX8/MX4 state")
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 
 def log(msg: str) -> None:
@@ -50,11 +51,13 @@ def parse_args():
                     help="MX cache layout: the reference's tensors (default) or the compact one "
                          "(bit micro-exponents, MX4 nibble mantissas; same arithmetic)")
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
-    ap.add_argument("--sweep", action="store_true",
+    ap.add_argument("--sweep", nargs="?", const="all", default=None,
+                    choices=["all", "attention", "state", "prefill"],
                     help="instead of the decode step, time each kernel alone over the BASELINE "
                          "configurations (attention: batch 1/8/64 x ctx 1K/4K/16K; MX8, MX4 and "
-                         "bf16 state updates: batch 1/8/64), each call after a 512 MB scratch "
-                         "read so that nothing is cache-resident; prints one JSON line")
+                         "bf16 state updates: batch 1/8/64; INT4 prefill: L 1K/4K/16K), each call "
+                         "after a 512 MB scratch read so that nothing is cache-resident; prints "
+                         "one JSON line. An argument restricts it to one kernel family")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy, the reference kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -178,10 +181,11 @@ def run_step(torch, args, attn, mamba, ev=None):
         M["step"] += 1
 
 
-def sweep(torch, dev, reps: int = 20):
+def sweep(torch, dev, which: str = "all", reps: int = 20):
     """Per-kernel cold-cache timings over the BASELINE configurations."""
     from layer_quant_amd import _abi
-    from layer_quant_amd.traffic import attention_bytes, mx_update_bytes, ssm_update_bytes
+    from layer_quant_amd.traffic import (attention_bytes, mx_update_bytes, prefill_flops,
+                                         ssm_update_bytes)
 
     scratch = torch.ones(512 << 20, dtype=torch.uint8, device=dev)
     gen = torch.Generator(device=dev).manual_seed(0)
@@ -212,7 +216,7 @@ def sweep(torch, dev, reps: int = 20):
 
     rows = []
     hq, hkv, d, g = 32, 8, 128, 32
-    for B in (1, 8, 64):
+    for B in ((1, 8, 64) if which in ("all", "attention") else ()):
         for S in (1024, 4096, 16384):
             kp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
             vp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
@@ -225,7 +229,7 @@ def sweep(torch, dev, reps: int = 20):
                             batch=B, ctx=S, group=g))
             del kp, vp, ks, vs
     nh, p_, n, ng = 128, 64, 128, 8
-    for B in (1, 8, 64):
+    for B in ((1, 8, 64) if which in ("all", "state") else ()):
         x = torch.randn(B, nh, p_, device=dev, generator=gen).to(torch.bfloat16)
         dt = torch.randn(B, nh, device=dev, generator=gen).to(torch.bfloat16)[:, :, None].expand(B, nh, p_)
         A = (-torch.exp(torch.rand(nh, device=dev, generator=gen) * 2))[:, None, None].expand(nh, p_, n)
@@ -254,6 +258,24 @@ def sweep(torch, dev, reps: int = 20):
                                                               out, True))
         rows.append(row("bf16_selective_state_update", ssm_update_bytes(B, nh, p_, n, ng), med, mean,
                         batch=B))
+    for L in ((1024, 4096, 16384) if which in ("all", "prefill") else ()):
+        # causal prefill over the packed cache of one attention layer, batch 1 (MFMA-bound)
+        kp = torch.randint(0, 256, (1, hkv, L, d // 2), dtype=torch.uint8, device=dev, generator=gen)
+        vp = torch.randint(0, 256, (1, hkv, L, d // 2), dtype=torch.uint8, device=dev, generator=gen)
+        ks = torch.rand(1, hkv, L, d // g, device=dev, generator=gen) + 0.01
+        vs = torch.rand(1, hkv, L, d // g, device=dev, generator=gen) + 0.01
+        q = torch.randn(1, hq, L, d, device=dev, generator=gen).to(torch.bfloat16)
+        out = torch.empty(1, hq, L, d, device=dev, dtype=torch.bfloat16)
+        med, mean = timed(lambda: _abi.int4_prefill_attention(q, kp, vp, ks, vs, out, 4, g))
+        fl = prefill_flops(1, hq, L, d)
+        tfs = fl / (med * 1e-6) / 1e12
+        rows.append(dict(kernel="int4_prefill_attention", batch=1, q_len=L, group=g,
+                         median_us=round(med, 2), mean_us=round(mean, 2), algorithmic_flops=fl,
+                         TFLOP_s=round(tfs, 1), frac_of_peak=round(tfs / PEAK_BF16_TFLOPS, 4),
+                         peak="bf16 dense MFMA"))
+        log(f"int4_prefill_attention L={L}: {med:.1f} us, {tfs:.0f} TFLOP/s "
+            f"({tfs / PEAK_BF16_TFLOPS:.1%} of bf16 MFMA)")
+        del kp, vp, ks, vs, q, out
     return {"sweep": rows, "reps": reps, "timing": "median of per-call HIP events, each call after a "
             "512 MB scratch read (a read evicts the caches without leaving dirty lines whose "
             "write-back would compete with the timed kernel)", "peak_GB_s": PEAK_HBM_GBS}
@@ -357,7 +379,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     if args.sweep:
-        print(json.dumps(sweep(torch, dev)), flush=True)
+        print(json.dumps(sweep(torch, dev, args.sweep)), flush=True)
         return
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)

@@ -4,7 +4,8 @@
  * One shared library (liblayer_quant.so) exports the entry points below. They replace the
  * Triton kernel launches of the reference's two quantized decode paths:
  *
- *   hybrid_quant/int4_8b_attention.py     INT4 KV cache: per-token pack + q_len=1 decode attention
+ *   hybrid_quant/int4_8b_attention.py     INT4 KV cache: per-token pack, q_len=1 decode attention
+ *                                         and causal prefill attention over the packed cache
  *   hybrid_quant/mamba_state_8b_kernel.py Mamba2 selective-state update over an MX8/MX4 state
  *
  * Conventions
@@ -120,6 +121,20 @@ int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
                              const lq_tensor* v_scale, const lq_tensor* mask, const lq_tensor* out,
                              int64_t seq_len, int num_key_value_groups, int group_size,
                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Causal INT4 prefill attention over the packed cache: query position t of q [B, Hq, L, D]
+ * attends to cache rows 0 .. t of KV head h / num_key_value_groups, scores (q . k) *
+ * log2(e)/sqrt(D) in an exp2-domain softmax; out [B, Hq, L, D] (f32/bf16/f16). Replaces
+ * _int4_prefill_attention_kernel and its launcher _prefill_attention (reference
+ * hybrid_quant/int4_8b_attention.py:114-251, 594-625). Requires L <= capacity; any strides on
+ * q and out; no workspace. MFMA path for head_dim 128, group 32/64/128 and bf16 q with
+ * contiguous cache rows; a generic path otherwise.
+ */
+int lq_int4_prefill_attention(const lq_tensor* q, const lq_tensor* k_packed,
+                              const lq_tensor* v_packed, const lq_tensor* k_scale,
+                              const lq_tensor* v_scale, const lq_tensor* out,
+                              int num_key_value_groups, int group_size, void* stream);
 
 /*
  * MX state layouts. Every MX entry point takes either layout and tells them apart by the shapes

@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "lq_int4_pack_kv",
     "lq_int4_decode_attention_workspace",
     "lq_int4_decode_attention",
+    "lq_int4_prefill_attention",
     "lq_mx_encode",
     "lq_mx_decode",
     "lq_mx_state_update",
@@ -87,6 +88,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.lq_int4_decode_attention.argtypes = [_P] * 7 + [
         ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
         ctypes.c_void_p]
+    lib.lq_int4_prefill_attention.restype = ctypes.c_int
+    lib.lq_int4_prefill_attention.argtypes = [_P] * 6 + [ctypes.c_int, ctypes.c_int,
+                                                          ctypes.c_void_p]
     lib.lq_mx_encode.restype = ctypes.c_int
     lib.lq_mx_encode.argtypes = [_P] * 4 + [ctypes.c_int, ctypes.c_int, _P, ctypes.c_uint64,
                                             ctypes.c_uint64, ctypes.c_void_p]
@@ -223,6 +227,18 @@ def int4_decode_attention(q: torch.Tensor, k_packed: torch.Tensor, v_packed: tor
         desc(out), int(seq_len), int(num_key_value_groups), int(group_size),
         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream)
     check(rc, "lq_int4_decode_attention")
+    return out
+
+
+def int4_prefill_attention(q: torch.Tensor, k_packed: torch.Tensor, v_packed: torch.Tensor,
+                           k_scale: torch.Tensor, v_scale: torch.Tensor, out: torch.Tensor,
+                           num_key_value_groups: int, group_size: int) -> torch.Tensor:
+    """Causal attention of q [B, Hq, L, D] over cache keys 0 .. t for position t -> out."""
+    dev = _require_gpu(q, k_packed, v_packed, k_scale, v_scale, out)
+    rc = lib().lq_int4_prefill_attention(desc(q), desc(k_packed), desc(v_packed), desc(k_scale),
+                                         desc(v_scale), desc(out), int(num_key_value_groups),
+                                         int(group_size), _stream(dev))
+    check(rc, "lq_int4_prefill_attention")
     return out
 
 

@@ -4,12 +4,13 @@ API-compatible with the reference module hybrid_quant/int4_8b_attention.py (cite
 the same public names, argument meaning and error messages, with the two Triton kernels replaced
 by HIP kernels for gfx950 behind the C ABI (include/layer_quant.h):
 
-    _pack_int4_kv_kernel           -> lq_int4_pack_kv           (ia.py:32-111)
-    _int4_decode_attention_kernel  -> lq_int4_decode_attention  (ia.py:254-402)
+    _pack_int4_kv_kernel            -> lq_int4_pack_kv            (ia.py:32-111)
+    _int4_decode_attention_kernel   -> lq_int4_decode_attention   (ia.py:254-402)
+    _int4_prefill_attention_kernel  -> lq_int4_prefill_attention  (ia.py:114-251)
 
-The reference's prefill kernel (ia.py:114-251, _prefill_attention at ia.py:594-625) is never
-called by the reference (prefill runs SDPA on unquantized K/V, ia.py:693-714) and is not
-provided.
+The reference never calls its prefill kernel (the patched forward runs SDPA on unquantized K/V
+for q_len > 1, ia.py:693-714, and so does this module); _prefill_attention keeps its
+signature (ia.py:594-625) for callers that attend over the packed cache instead.
 """
 from __future__ import annotations
 
@@ -161,6 +162,18 @@ def _decode_attention(query_states: torch.Tensor, cache: Int4KVLayerCache, seq_l
     _abi.int4_decode_attention(query_states, cache.k_packed, cache.v_packed, cache.k_scale,
                                cache.v_scale, mask, out, seq_len, num_key_value_groups,
                                group_size)
+    return out
+
+
+def _prefill_attention(query_states: torch.Tensor, cache: Int4KVLayerCache,
+                       num_key_value_groups: int, group_size: int) -> torch.Tensor:
+    """Causal attention of q [B, Hq, L, D] over cache rows [0, L): position t attends to rows
+    0 .. t -> [B, Hq, L, D] in q's dtype (ia.py:594-625)."""
+    batch, n_heads, q_len, head_dim = query_states.shape
+    out = torch.empty((batch, n_heads, q_len, head_dim), device=query_states.device,
+                      dtype=query_states.dtype)
+    _abi.int4_prefill_attention(query_states, cache.k_packed, cache.v_packed, cache.k_scale,
+                                cache.v_scale, out, num_key_value_groups, group_size)
     return out
 
 

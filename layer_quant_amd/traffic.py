@@ -1,5 +1,6 @@
 """Algorithmic (unique) HBM bytes of one call of each kernel: every input read once, every output
-written once. These are the byte counts behind the GB/s and roofline figures bench.py reports."""
+written once, and the algorithmic flops of the MFMA-bound prefill. These are the figures behind
+the GB/s, TFLOP/s and roofline fractions bench.py reports."""
 from __future__ import annotations
 
 
@@ -53,3 +54,9 @@ def ssm_update_bytes(batch: int, nheads: int, dim: int, dstate: int, ngroups: in
     bc = 2 * batch * ngroups * dstate * 2
     scalars = batch * nheads * dt_bytes + 3 * nheads * 4
     return 2 * elems * state_bytes + io + bc + scalars
+
+
+def prefill_flops(batch: int, n_q_heads: int, q_len: int, head_dim: int) -> int:
+    """Causal prefill attention: 2*D flops for q.k and 2*D for p*v per visible (query, key)
+    pair, L (L + 1) / 2 pairs per (batch, head)."""
+    return 4 * head_dim * batch * n_q_heads * (q_len * (q_len + 1) // 2)

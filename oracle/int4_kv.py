@@ -13,6 +13,10 @@ Pinning (tests/test_oracle_int4.py):
                       routine); seq_len=1 -> V row 0; q=0 -> mean of V; masked keys excluded;
                       GQA head mapping kvh = qh // n_rep
   decode_attention_mask  each branch of ia.py:569-591 against hand-built masks
+  prefill_attention   torch scaled_dot_product_attention(is_causal=True) on the dequantized cache
+                      (library routine); row t equals decode_attention over t + 1 keys (the causal
+                      length q_pos + 1 of ia.py:170); a per-element loop on tiny inputs; q_len=1 ->
+                      V row 0; q=0 -> running mean of V
 """
 from __future__ import annotations
 
@@ -128,6 +132,38 @@ def decode_attention(q: torch.Tensor, k_packed: torch.Tensor, v_packed: torch.Te
     m = s.amax(dim=-1, keepdim=True)
     p = torch.exp2(s - m)
     return torch.einsum("bhs,bhsd->bhd", p, v) / p.sum(dim=-1, keepdim=True)
+
+
+def prefill_attention(q: torch.Tensor, k_packed: torch.Tensor, v_packed: torch.Tensor,
+                      k_scale: torch.Tensor, v_scale: torch.Tensor, num_key_value_groups: int,
+                      group_size: int) -> torch.Tensor:
+    """Causal multi-token attention over the packed cache, in float64 (ia.py:114-251, launched by
+    _prefill_attention at ia.py:594-625).
+
+    q: [B, Hq, L, D]. Query position t of head h attends to cache keys 0 .. t of KV head
+    h // num_key_value_groups (causal_len = q_pos + 1, ia.py:166-170; the cache holds the prompt
+    from position 0). Scores (q . k_n) * log2(e)/sqrt(D), exp2-domain softmax (ia.py:162,
+    209-213), out = sum p_n v_n / sum p_n (ia.py:243). Returns float64 [B, Hq, L, D].
+    """
+    bsz, hq, q_len, d = q.shape
+    k = dequantize(k_packed[:, :, :q_len], k_scale[:, :, :q_len], group_size).double()
+    v = dequantize(v_packed[:, :, :q_len], v_scale[:, :, :q_len], group_size).double()
+    kv_index = torch.arange(hq) // num_key_value_groups
+    k = k[:, kv_index]  # [B, Hq, L, D]
+    v = v[:, kv_index]
+    scale_sm = 1.4426950408889634 / math.sqrt(d)
+    s = torch.matmul(q.double(), k.transpose(-1, -2).contiguous()) * scale_sm  # [B, Hq, L, L]
+    future = torch.ones(q_len, q_len, dtype=torch.bool).triu(1)
+    s = s.masked_fill(future, -math.inf)
+    m = s.amax(dim=-1, keepdim=True)
+    p = torch.exp2(s - m)
+    return torch.matmul(p, v) / p.sum(dim=-1, keepdim=True)
+
+
+def prefill_flops(batch: int, n_q_heads: int, q_len: int, head_dim: int) -> int:
+    """Algorithmic flops of one causal prefill call: 2*D for q.k and 2*D for p*v per visible
+    (query, key) pair, L (L + 1) / 2 pairs per head."""
+    return 4 * head_dim * batch * n_q_heads * (q_len * (q_len + 1) // 2)
 
 
 def decode_attention_mask(attention_mask: torch.Tensor | None, batch: int,

@@ -88,6 +88,33 @@ def test_attention_rejects_bad_arguments():
                                         0, None) == _abi.LQ_ERR_WORKSPACE
 
 
+def test_prefill_rejects_bad_arguments():
+    lib = _abi.lib()
+    kp = _fake((2, 8, 64, 64), torch.uint8)
+    ks = _fake((2, 8, 64, 4), torch.float32)
+    q = _fake((2, 32, 48, 128), torch.bfloat16)
+    out = _fake((2, 32, 48, 128), torch.bfloat16)
+    long_q = _fake((2, 32, 65, 128), torch.bfloat16)
+    long_out = _fake((2, 32, 65, 128), torch.bfloat16)
+    assert lib.lq_int4_prefill_attention(long_q, kp, kp, ks, ks, long_out, 4, 32,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+    assert "capacity" in _abi.last_error()
+    assert lib.lq_int4_prefill_attention(q, kp, kp, ks, ks, out, 3, 32,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+    assert lib.lq_int4_prefill_attention(q, kp, kp, ks, ks, out, 4, 31,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+    short_out = _fake((2, 32, 47, 128), torch.bfloat16)
+    assert lib.lq_int4_prefill_attention(q, kp, kp, ks, ks, short_out, 4, 32,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+    assert "out must be" in _abi.last_error()
+    bad_ks = _fake((2, 8, 64, 2), torch.float32)
+    assert lib.lq_int4_prefill_attention(q, kp, kp, bad_ks, ks, out, 4, 32,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+    q3 = _fake((2, 32, 128), torch.bfloat16)
+    assert lib.lq_int4_prefill_attention(q3, kp, kp, ks, ks, out, 4, 32,
+                                         None) == _abi.LQ_ERR_INVALID_ARG
+
+
 def test_mx_rejects_bad_arguments():
     lib = _abi.lib()
     qs = _fake((2, 4, 8, 128), torch.int8)

@@ -182,3 +182,56 @@ def test_package_byte_counts_match_the_oracle():
     for args in [(64, 32, 8, 128, 16384, 32), (1, 32, 8, 128, 1024, 32), (8, 32, 8, 128, 4096, 64)]:
         assert traffic.attention_bytes(*args) == ik.algorithmic_bytes(*args)
     assert traffic.pack_bytes(64, 8, 1, 128, 32) == ik.pack_algorithmic_bytes(64, 8, 1, 128, 32)
+    assert traffic.prefill_flops(1, 32, 16384, 128) == ik.prefill_flops(1, 32, 16384, 128)
+
+
+@pytest.mark.parametrize("nrep,g,L", [(4, 32, 23), (2, 64, 40), (1, 16, 7)])
+def test_prefill_matches_causal_sdpa(nrep, g, L):
+    b, hkv, d = 2, 2, 128
+    c = _cache(b, hkv, L + 5, d, g, 30)  # capacity above L: rows past L must not be read
+    q = torch.randn(b, hkv * nrep, L, d, generator=torch.Generator().manual_seed(31))
+    out = ik.prefill_attention(q, c["k_packed"], c["v_packed"], c["k_scale"], c["v_scale"], nrep, g)
+    kd = ik.dequantize(c["k_packed"][:, :, :L], c["k_scale"][:, :, :L], g).double()
+    vd = ik.dequantize(c["v_packed"][:, :, :L], c["v_scale"][:, :, :L], g).double()
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.double(), kd.repeat_interleave(nrep, 1), vd.repeat_interleave(nrep, 1), is_causal=True)
+    assert out.shape == (b, hkv * nrep, L, d)
+    assert torch.allclose(out, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_prefill_row_is_decode_over_its_prefix():
+    b, hkv, nrep, d, g, L = 1, 2, 4, 128, 32, 19
+    c = _cache(b, hkv, L, d, g, 32)
+    args = (c["k_packed"], c["v_packed"], c["k_scale"], c["v_scale"])
+    q = torch.randn(b, hkv * nrep, L, d, generator=torch.Generator().manual_seed(33))
+    out = ik.prefill_attention(q, *args, nrep, g)
+    for t in (0, 1, 7, L - 1):
+        dec = ik.decode_attention(q[:, :, t], *args, t + 1, nrep, g)
+        assert torch.allclose(out[:, :, t], dec, rtol=1e-12, atol=1e-13), t
+
+
+def test_prefill_element_loop_and_special_cases():
+    b, hkv, nrep, d, g, L = 1, 1, 2, 8, 4, 5
+    c = _cache(b, hkv, L, d, g, 34)
+    args = (c["k_packed"], c["v_packed"], c["k_scale"], c["v_scale"])
+    q = torch.randn(b, hkv * nrep, L, d, generator=torch.Generator().manual_seed(35))
+    out = ik.prefill_attention(q, *args, nrep, g)
+    kd = ik.dequantize(c["k_packed"], c["k_scale"], g).double()
+    vd = ik.dequantize(c["v_packed"], c["v_scale"], g).double()
+    for h in range(hkv * nrep):
+        for t in range(L):
+            w = [math.exp(sum(q[0, h, t, i].item() * kd[0, h // nrep, n, i].item()
+                              for i in range(d)) / math.sqrt(d)) for n in range(t + 1)]
+            for i in range(d):
+                want = sum(w[n] * vd[0, h // nrep, n, i].item() for n in range(t + 1)) / sum(w)
+                assert abs(out[0, h, t, i].item() - want) <= 1e-12 * (1 + abs(want))
+    one = ik.prefill_attention(q[:, :, :1], *args, nrep, g)  # q_len 1: V row 0
+    assert torch.allclose(one[:, :, 0], vd[:, :, 0].repeat_interleave(nrep, 1), atol=1e-12)
+    zero = ik.prefill_attention(torch.zeros_like(q), *args, nrep, g)  # uniform: running mean
+    run = vd.cumsum(2) / torch.arange(1, L + 1, dtype=torch.float64)[:, None]
+    assert torch.allclose(zero, run.repeat_interleave(nrep, 1), atol=1e-12)
+
+
+def test_prefill_flops_closed_form():
+    assert ik.prefill_flops(1, 32, 16384, 128) == 4 * 128 * 32 * (16384 * 16385 // 2)
+    assert ik.prefill_flops(2, 1, 1, 64) == 2 * 4 * 64
