@@ -104,8 +104,10 @@ struct alignas(16) PrefillLds {
 };
 
 // One thread's share of a tile's global reads: 8 bytes of K (key tid/8, dwords 2u, 2u+1),
-// dword tid%16 of the V rows of keys 2(tid/16), 2(tid/16)+1, and one scale word (K scales on
-// threads 0..127, V scales on 128..255). Keys at or past L read as zero.
+// dword tid/16 of the V rows of keys 2(tid%16), 2(tid%16)+1 (consecutive lanes take consecutive
+// key pairs, so the transposed LDS writes of a wave fill whole rows instead of hitting one bank
+// per row 8 apart), and one scale word (K scales on threads 0..127, V scales on 128..255). Keys
+// at or past L read as zero.
 struct RawTile {
   uint32_t k0, k1;
   uint32_t v0, v1;
@@ -124,9 +126,9 @@ __device__ __forceinline__ void load_tile(const uint8_t* kb, const uint8_t* vb, 
     r.k0 = 0;
     r.k1 = 0;
   }
-  const int vk = tb + 2 * (tid >> 4);
-  r.v0 = vk < L ? *(const uint32_t*)(vb + (int64_t)vk * 64 + 4 * (tid & 15)) : 0u;
-  r.v1 = vk + 1 < L ? *(const uint32_t*)(vb + (int64_t)(vk + 1) * 64 + 4 * (tid & 15)) : 0u;
+  const int vk = tb + 2 * (tid & 15);
+  r.v0 = vk < L ? *(const uint32_t*)(vb + (int64_t)vk * 64 + 4 * (tid >> 4)) : 0u;
+  r.v1 = vk + 1 < L ? *(const uint32_t*)(vb + (int64_t)(vk + 1) * 64 + 4 * (tid >> 4)) : 0u;
   const int si = tid & 127;
   const int sk = tb + si / G;
   const float* sb = tid < 128 ? ksb : vsb;
@@ -147,8 +149,8 @@ __device__ __forceinline__ void stage_tile(PrefillLds<G>& s, int nb, const RawTi
     *(u32x4_t*)&s.k[nb][key][16 * u + 8] = decode_octet_f16(r.k1);
   }
   {
-    const int k0 = 2 * (tid >> 4);
-    const int w = tid & 15;
+    const int k0 = 2 * (tid & 15);
+    const int w = tid >> 4;
     const int col = vcol(k0);
     // ylo = bytes (k0.b0, k0.b1, k1.b0, k1.b1), yhi = (k0.b2, k0.b3, k1.b2, k1.b3): nibble i of
     // ylo and of ylo >> 16 is dim 8w + i of key k0 and of key k0 + 1
