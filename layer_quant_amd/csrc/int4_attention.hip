@@ -135,47 +135,69 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// One wave per (batch, query head): M = max_s m_s and L = sum_s 2^(m_s - M) l_s from
-// lane-parallel loads and wave reductions, then out = sum_s 2^(m_s - M) acc_s / L with the
-// per-split partial rows loaded four splits at a time.
-__global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams p) {
-  const int lane = threadIdx.x;
+// One 256-thread workgroup per (batch, query head), so that every split's partial row is loaded
+// in parallel (a single wave walking the splits one after another paid a memory round trip per
+// few splits, which dominated small batches at long contexts): M = max_s m_s and
+// L = sum_s 2^(m_s - M) l_s by block reductions, then thread (g, d) sums 2^(m_s - M) acc_s[d] over
+// the splits s = g mod G (G = 256 / D split groups for D <= 256; each thread takes two dims of one
+// group for larger D), and the group partials are summed through LDS.
+constexpr int MERGE_THREADS = 256;
+
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+  v = is_max ? wave_max(v) : wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < MERGE_THREADS / 64; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(MERGE_THREADS) void attn_merge_kernel(AttnParams p) {
+  __shared__ float red[MERGE_THREADS / 64];
+  __shared__ float part[MERGE_THREADS];
+  const int tid = threadIdx.x;
   const int bh = blockIdx.x;
   const int b = bh / p.Hq;
   const int qh = bh - b * p.Hq;
   const int64_t base = (int64_t)bh * p.nsplit;
   const int ns = p.nsplit;
+  const int D = p.D;
   float M = -INFINITY;
-  for (int s = lane; s < ns; s += 64) M = fmaxf(M, p.ws_m[base + s]);
-  M = wave_max(M);
+  for (int s = tid; s < ns; s += MERGE_THREADS) M = fmaxf(M, p.ws_m[base + s]);
+  M = block_reduce(M, true, red);
   float L = 0.0f;
-  for (int s = lane; s < ns; s += 64) {
+  for (int s = tid; s < ns; s += MERGE_THREADS) {
     const float ms = p.ws_m[base + s];
     L += (ms == -INFINITY) ? 0.0f : exp2f(ms - M) * p.ws_l[base + s];
   }
-  L = wave_sum(L);
-  const int nd = (p.D + 63) >> 6;
-  float acc[GEN_MAX_D / 64];
-#pragma unroll
-  for (int i = 0; i < GEN_MAX_D / 64; ++i) acc[i] = 0.0f;
-#pragma unroll 4
-  for (int s = 0; s < ns; ++s) {
-    const float ms = p.ws_m[base + s];
-    const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
-    const float* a = p.ws_acc + (base + s) * p.D;
-#pragma unroll
-    for (int i = 0; i < GEN_MAX_D / 64; ++i) {
-      const int d = lane + 64 * i;
-      if (i < nd && d < p.D) acc[i] += w * a[d];
+  L = block_reduce(L, false, red);
+
+  const int dw = min(D, MERGE_THREADS);  // dims per pass
+  const int groups = MERGE_THREADS / dw;  // split groups
+  const int g = tid / dw;
+  const int d0 = tid - g * dw;
+  const int64_t obase = b * p.out.s[0] + qh * p.out.s[1];
+  for (int d = d0; d < D; d += dw) {
+    float acc = 0.0f;
+    if (g < groups) {
+      for (int s = g; s < ns; s += groups) {
+        const float ms = p.ws_m[base + s];
+        const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
+        acc += w * p.ws_acc[(base + s) * D + d];
+      }
     }
-  }
-#pragma unroll
-  for (int i = 0; i < GEN_MAX_D / 64; ++i) {
-    const int d = lane + 64 * i;
-    if (i < nd && d < p.D) {
-      store_float(p.out.data, p.out.dtype, b * p.out.s[0] + qh * p.out.s[1] + d * p.out.s[2],
-                  acc[i] / L);
+    if (groups > 1) {
+      part[tid] = acc;
+      __syncthreads();
+      if (g == 0) {
+        for (int i = 1; i < groups; ++i) acc += part[i * dw + d0];
+      }
+      __syncthreads();
     }
+    if (g == 0) store_float(p.out.data, p.out.dtype, obase + d * p.out.s[2], acc / L);
   }
 }
 
@@ -352,7 +374,7 @@ extern "C" int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_p
     if ((rc = check_launch("lq_int4_decode_attention")) != LQ_OK) return rc;
   }
   if (p.nsplit > 1) {
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * Hq)), dim3(64), 0, st, p);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * Hq)), dim3(MERGE_THREADS), 0, st, p);
     if ((rc = check_launch("lq_int4_decode_attention merge")) != LQ_OK) return rc;
   }
   return LQ_OK;
