@@ -19,8 +19,9 @@
 // 136 + n, so the accumulator starts at -136 * sum(q) of the column's dims.
 //
 // P V. A = V^T: 16 dims x 32 keys, B = P' with P'[key][(m, h)] = p[key][h] * vscale[key][m].
-// Lane (q, c) loads dword c of key rows q + 4e (e = 0..7; one load instruction reads 4 whole
-// consecutive rows), so MFMA k (k = 0..7) covers dims 8c + k; the output
+// Lane (q, c) needs dword c of key rows q + 4e (e = 0..7), so MFMA k (k = 0..7) covers dims
+// 8c + k. The V rows arrive as 128-bit loads (32-bit loads cap the stream near 4.2 TB/s on MI355X
+// against 7 TB/s for 128-bit) and pass through a per-wave LDS buffer into that layout; the output
 // column (m, h) is kept only for dims of group m. P' is split into bf16 hi + lo (two MFMAs, about
 // 16 significant bits). The value offset 136 of the V decode is removed at the end with
 // sum_keys P' from one more MFMA against a ones operand.
@@ -36,6 +37,7 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int FAST_D = 128;
 constexpr int SUB = 32;              // keys per MFMA sub-tile (the K depth of the P V product)
@@ -91,12 +93,29 @@ __device__ __forceinline__ float column_sum(float x) {
 
 template <int G>
 struct TileRegs {
-  static constexpr int SCW = (G * TILE + 63) / 64;  // scale words per lane
   u32x4_t kq[NSUB][2];      // [sub][16-key half]: 16-byte unit l/16 (dims 32*(l/16) ..) of row l%16
-  uint32_t vw[NSUB][8];     // [sub]: dword l%16 of the 8 key rows of this lane's K slots
-  float ksr[SCW];           // key / value scale words, staged through LDS
-  float vsr[SCW];
+  u32x4_t vq[NSUB][2];      // [sub][16-key half]: 16-byte unit l%4 of V row l/4
+  float ksr[G];             // key / value scales of key row l%32, staged through LDS
+  float vsr[G];
 };
+
+// G consecutive fp32 scale words at byte offset off, as one buffer load. (The words are
+// reinterpreted with __uint_as_float: with this compiler, __builtin_bit_cast(float, w[m]) of a
+// vector element narrowed the 128-bit load to its first dword and lost the other three.)
+template <int G>
+__device__ __forceinline__ void load_scales(__amdgpu_buffer_rsrc_t r, int off, float (&v)[G]) {
+  if constexpr (G == 4) {
+    const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, KV_LOAD_POLICY);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) v[m] = __uint_as_float(w[m]);
+  } else if constexpr (G == 2) {
+    const u32x2_t w = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, KV_LOAD_POLICY);
+    v[0] = __uint_as_float(w[0]);
+    v[1] = __uint_as_float(w[1]);
+  } else {
+    v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, KV_LOAD_POLICY));
+  }
+}
 
 // Per-wave bases of this (batch, KV head) block; rows are contiguous (64 packed bytes, G scale
 // words). Each tile builds buffer descriptors whose base is the tile's first key and whose size
@@ -107,7 +126,7 @@ struct Rsrc {
   const uint8_t* vb;
   const float* ksb;
   const float* vsb;
-  int kvo, vvo;  // per-lane byte offsets inside a tile
+  int kvo, vvo, svo;  // per-lane byte offsets inside a tile (K unit, V unit, scale row)
 };
 
 template <int G>
@@ -122,24 +141,16 @@ __device__ __forceinline__ void load_tile(const Rsrc& R, int tb, int S, TileRegs
       (void*)(R.ksb + (int64_t)tb * G), 0, rem * G * 4, BUF_DWORD3);
   const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(R.vsb + (int64_t)tb * G), 0, rem * G * 4, BUF_DWORD3);
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < TileRegs<G>::SCW; ++i) {
-    const int off = (lane + 64 * i) * 4;  // word (key, group) = key * G + group
-    r.ksr[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, off, 0, KV_LOAD_POLICY));
-    r.vsr[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, off, 0, KV_LOAD_POLICY));
-  }
+  load_scales<G>(rks, R.svo, r.ksr);  // lanes l and l + 32 read the same row
+  load_scales<G>(rvs, R.svo, r.vsr);
 #pragma unroll
   for (int sb = 0; sb < NSUB; ++sb) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       r.kq[sb][t] = __builtin_bit_cast(
           u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, R.kvo + (SUB * sb + 16 * t) * 64, 0, KV_LOAD_POLICY));
-
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      r.vw[sb][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, R.vvo + (SUB * sb + 4 * e) * 64, 0, KV_LOAD_POLICY);
+      r.vq[sb][t] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, R.vvo + (SUB * sb + 16 * t) * 64, 0, KV_LOAD_POLICY));
     }
   }
 }
@@ -150,6 +161,7 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
   constexpr int CPG = 4 / G;  // 32-dim chunks per group
   static_assert(NCOL <= 16, "columns exceed the MFMA tile");
   __shared__ float sc_lds[WAVES][2][2][G][TILE];  // [wave][buffer][k/v][group][key]
+  __shared__ u32x4_t v_lds[WAVES][TILE][4];         // [wave][key][16-byte unit]: one V tile
   __shared__ float o_lds[WAVES][NREP][FAST_D];
   __shared__ float ml_lds[WAVES][2][NREP];
 
@@ -208,7 +220,8 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
   // lane group q) is key 4r + q, and lane group q's 8 keys of a 32-key sub-tile are q + 4e
   // (e = 4t + r): the V loads of key slot e then cover keys 4e .. 4e+3 contiguously.
   R.kvo = (4 * (c16 & 3) + (c16 >> 2)) * 64 + 16 * q4;
-  R.vvo = q4 * 64 + 4 * c16;
+  R.vvo = (lane >> 2) * 64 + 16 * (lane & 3);
+  R.svo = (lane & 31) * G * 4;
 
   float m_run = -INFINITY;
   float l_run = 0.0f;
@@ -221,16 +234,14 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
   // Scales of a tile go to LDS, transposed to [group][key] with log2(e)/sqrt(D) folded into the
   // key scales, one tile before their use; buffer (tile index & 1).
   auto stage_scales = [&](const TileRegs<G>& r, const int buf) {
+    if (lane < TILE) {
+      const int tok = lane;
+      // key 16t + 4r + q is read by lane group q as element r: store it at 16t + 4q + r
+      const int pos = (tok & ~15) | ((tok & 3) << 2) | ((tok >> 2) & 3);
 #pragma unroll
-    for (int i = 0; i < TileRegs<G>::SCW; ++i) {
-      const int idx = lane + 64 * i;
-      if (idx < G * TILE) {
-        const int tok = idx / G;
-        const int m = idx - tok * G;
-        // key 16t + 4r + q is read by lane group q as element r: store it at 16t + 4q + r
-        const int pos = (tok & ~15) | ((tok & 3) << 2) | ((tok >> 2) & 3);
-        sc_lds[wave][buf][0][m][pos] = r.ksr[i] * p.scale_sm;
-        sc_lds[wave][buf][1][m][pos] = r.vsr[i];
+      for (int m = 0; m < G; ++m) {
+        sc_lds[wave][buf][0][m][pos] = r.ksr[m] * p.scale_sm;
+        sc_lds[wave][buf][1][m][pos] = r.vsr[m];
       }
     }
   };
@@ -339,12 +350,19 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
         bhi[u] = h;
         blo[u] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t));
       }
+      // V rows through this wave's LDS buffer: dword c16 of key rows q4 + 4e (e = 0..7)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) v_lds[wave][16 * t + (lane >> 2)][lane & 3] = cur.vq[sb][t];
+      const uint32_t* vrow = (const uint32_t*)&v_lds[wave][0][0];
+      uint32_t vw[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vw[e] = vrow[(q4 + 4 * e) * 16 + c16];
       // V decode: pair the key slots (2u, 2u+1), nibble k of each dword -> MFMA k
       uint32_t ylo[4], yhi[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        ylo[u] = __builtin_amdgcn_perm(cur.vw[sb][2 * u + 1], cur.vw[sb][2 * u], 0x05040100u);
-        yhi[u] = __builtin_amdgcn_perm(cur.vw[sb][2 * u + 1], cur.vw[sb][2 * u], 0x07060302u);
+        ylo[u] = __builtin_amdgcn_perm(vw[2 * u + 1], vw[2 * u], 0x05040100u);
+        yhi[u] = __builtin_amdgcn_perm(vw[2 * u + 1], vw[2 * u], 0x07060302u);
       }
       // four dims-sets at a time: their hi products, then their lo products, so that the two
       // MFMAs into one accumulator are separated by three independent ones
@@ -367,7 +385,8 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
     __builtin_amdgcn_wave_barrier();
   };
 
-  // three register stages: two tiles of loads stay in flight while a third is processed
+  // three register stages: two tiles of loads stay in flight while a third is processed (a
+  // fourth stage measured the same)
   TileRegs<G> ra, rb, rc;
   if (w0 < w1) {
     load_tile<G>(R, w0, S, ra);
