@@ -130,9 +130,9 @@ __device__ __forceinline__ void load_tile(const uint8_t* kb, const uint8_t* vb, 
   r.v0 = vk < L ? *(const uint32_t*)(vb + (int64_t)vk * 64 + 4 * (tid >> 4)) : 0u;
   r.v1 = vk + 1 < L ? *(const uint32_t*)(vb + (int64_t)(vk + 1) * 64 + 4 * (tid >> 4)) : 0u;
   const int si = tid & 127;
-  const int sk = tb + si / G;
+  const int sk = tb + (si & (KT - 1));  // scale word (key si % 32, group si / 32)
   const float* sb = tid < 128 ? ksb : vsb;
-  r.sc = (si < G * KT && sk < L) ? sb[(int64_t)sk * G + (si % G)] : 0.0f;
+  r.sc = (si < G * KT && sk < L) ? sb[(int64_t)sk * G + (si / KT)] : 0.0f;
 }
 
 // key k of a tile -> its column in the V^T tile: lane group j's keys 4j..4j+3 and 16+4j..16+4j+3
@@ -163,9 +163,9 @@ __device__ __forceinline__ void stage_tile(PrefillLds<G>& s, int nb, const RawTi
     }
   }
   const int si = tid & 127;
-  if (si < G * KT) {
-    const int key = si / G;
-    const int m = si - key * G;
+  if (si < G * KT) {  // consecutive lanes write consecutive keys of one group (no bank conflict)
+    const int key = si & (KT - 1);
+    const int m = si / KT;
     if (tid < 128) {
       s.ks[nb][m][key] = r.sc * scale_sm;
     } else {
