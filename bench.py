@@ -253,6 +253,19 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
             rows.append(row(f"mx{bits}_state_update", mx_update_bytes(
                 B, nh, p_, n, ng, format_bits=bits, layout=layout), med, mean, batch=B,
                 layout=layout, rounding="stochastic (counter)"))
+        # the BASELINE configurations' seeded uniform tensor (reference formula, bit-exact mode):
+        # the fp32 tensor adds 4 bytes per state element to the traffic
+        uni = torch.rand(B, nh, p_, n, device=dev, generator=gen)
+        for bits in (8, 4):
+            st = _mx_tensors(torch, (B, nh, p_, n), bits, "reference", dev)
+            _abi.mx_encode(h0, *st, bits, _abi.ROUND_NEAREST_EVEN)
+            med, mean = timed(lambda: _abi.mx_state_update(*st, x, dt, dtb, A, Bm, Cm, D, None, out,
+                                                           bits, True, _abi.ROUND_SR_UNIFORM,
+                                                           uniform=uni))
+            rows.append(row(f"mx{bits}_state_update", mx_update_bytes(
+                B, nh, p_, n, ng, format_bits=bits) + 4 * uni.numel(), med, mean, batch=B,
+                layout="reference", rounding="stochastic (supplied uniform tensor)"))
+        del uni
         state = h0.to(torch.bfloat16)
         med, mean = timed(lambda: _abi.selective_state_update(state, x, dt, dtb, A, Bm, Cm, D, None,
                                                               out, True))

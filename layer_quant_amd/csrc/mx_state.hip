@@ -54,6 +54,9 @@ struct MxUpdateParams {
   // (batch, head) slice of each rounded up to 4 (0 for an absent z)
   uint32_t x_row_bytes, z_row_bytes, out_row_bytes;
   uint32_t x_span, z_span, out_span;
+  // rows kernel, supplied-uniform mode: byte stride between rows of the uniform tensor and the
+  // byte span of one (batch, head) slice of it
+  uint32_t uni_row_bytes, uni_span;
 };
 
 struct MxCodecParams {
@@ -597,11 +600,12 @@ template <int R>
 struct RowLoads {
   uint32_t q[R][4], m[R][2];  // raw block words (layout-dependent, see LayoutOf)
   uint32_t e[R], xw[R], zw[R];
+  u32x4_t u[R][4];            // the block's 16 supplied uniforms (LQ_ROUND_SR_UNIFORM only)
 };
 
 // Buffer descriptors of one (batch, head) slice.
 struct HeadBufs {
-  __amdgpu_buffer_rsrc_t q, m, e, x, z, out;
+  __amdgpu_buffer_rsrc_t q, m, e, x, z, out, u;
 };
 
 template <uint32_t N, int LY>
@@ -617,13 +621,14 @@ __device__ __forceinline__ HeadBufs head_bufs(const MxUpdateParams& p, int b, in
   hb.x = make_buf(vbase(p.x, b, h), p.x_span);
   hb.z = make_buf(vbase(p.z, b, h), p.z_span);  // span 0 without z: its loads return 0
   hb.out = make_buf(vbase(p.out, b, h), p.out_span);
+  hb.u = make_buf(vbase(p.uni, b, h), p.uni_span);  // span 0 outside the uniform mode
   return hb;
 }
 
 // Issues the loads of rows row0 + r * SLOTS + slot (clamped to P - 1) of one slice.
 // (qo = pc * N + n0 is the block's mantissa offset in the reference layout; every other offset is
 // a shift of it.)
-template <int R, int SLOTS, uint32_t N, int LY>
+template <int R, int SLOTS, uint32_t N, int LY, int RMODE>
 __device__ __forceinline__ void load_rows(const MxUpdateParams& p, const HeadBufs& hb, int row0,
                                           int slot, uint32_t n0, RowLoads<R>& L) {
   using Lay = LayoutOf<LY>;
@@ -648,6 +653,14 @@ __device__ __forceinline__ void load_rows(const MxUpdateParams& p, const HeadBuf
     L.e[r] = __builtin_amdgcn_raw_buffer_load_b8(hb.e, qo >> 4, 0, STATE_LOAD_POLICY);
     L.xw[r] = __builtin_amdgcn_raw_buffer_load_b32(hb.x, (pc * p.x_row_bytes) & ~3u, 0, 0);
     L.zw[r] = __builtin_amdgcn_raw_buffer_load_b32(hb.z, (pc * p.z_row_bytes) & ~3u, 0, 0);
+    if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {
+      // the uniforms are read once: streaming loads, issued with the state's
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        L.u[r][j] = __builtin_amdgcn_raw_buffer_load_b128(hb.u, pc * p.uni_row_bytes + n0 * 4u + 16u * j,
+                                                          0, STATE_LOAD_POLICY);
+      }
+    }
   }
 }
 
@@ -715,7 +728,13 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
       encode16_dither<FB, LY>(hv, pw, qo, mo, eo);
     } else {
       float u16[16];
-      block_u16<RMODE>(p.uni, b, h, (int)pc, (int)n0, u16);
+      if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) u16[i] = __uint_as_float(L.u[r][i >> 2][i & 3]) * 65536.0f;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) u16[i] = 0.0f;
+      }
       encode16<FB, RMODE, LY>(hv, u16, qo, mo, eo);
     }
     if (act) {
@@ -755,7 +774,7 @@ void mx_update_rows_kernel(MxUpdateParams p) {
 
   const HeadBufs hb = head_bufs<N, LY>(p, b, h);
   RowLoads<R> L;
-  load_rows<R, SLOTS, N, LY>(p, hb, row0, slot, n0, L);
+  load_rows<R, SLOTS, N, LY, RMODE>(p, hb, row0, slot, n0, L);
   u32x4_t bw[2], cw[2];
   load_bc(p, b, h / p.ratio, n0, N, bw, cw);
   const HeadScalars hs = head_scalars(p, b, h);
@@ -1097,6 +1116,15 @@ static bool rows_path_ok(const MxUpdateParams& p, bool vec, bool bcvec, const lq
   if (p.x.s[2] < 0 || p.out.s[2] < 0 || p.z.s[2] < 0) return false;
   if (dt_bias != nullptr && dt_bias->stride[1] != 0) return false;
   if (D != nullptr && D->stride[1] != 0) return false;
+  if (round_mode == LQ_ROUND_SR_UNIFORM) {
+    // contiguous along d_state, 16-byte aligned rows, 32-bit slice spans
+    const View& u = p.uni;
+    if (u.s[3] != 1 || u.s[2] < p.N || (u.s[2] * 4) % 16 != 0 || u.s[0] % 4 != 0 || u.s[1] % 4 != 0) {
+      return false;
+    }
+    if (((uintptr_t)u.data & 15) != 0) return false;
+    if (((p.P - 1) * u.s[2] + p.N) * 4 >= lim) return false;
+  }
   if (round_mode == LQ_ROUND_SR_COUNTER) {
     if (p.rng_offset % 16 != 0 || total >= ((int64_t)1 << 32)) return false;
     const uint64_t first = p.rng_offset >> 1;
@@ -1232,6 +1260,14 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
       p.z = p.x;
       p.z_row_bytes = 0;
       p.z_span = 0;
+    }
+    if (round_mode == LQ_ROUND_SR_UNIFORM) {
+      p.uni_row_bytes = (uint32_t)(p.uni.s[2] * 4);
+      p.uni_span = (uint32_t)(((P - 1) * p.uni.s[2] + N) * 4);
+    } else {  // a zero-span descriptor: never read
+      p.uni = p.x;
+      p.uni_row_bytes = 0;
+      p.uni_span = 0;
     }
     // absent dt_bias or D: read dt's first element instead (the value is not used)
     const View dt0{p.dt.data, p.dt.dtype, {0, 0, 0, 0}};

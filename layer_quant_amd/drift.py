@@ -1,12 +1,15 @@
 """Long-chain state drift of the MX4 / MX8 recurrent state against an unquantized state.
 
     python -m layer_quant_amd.drift [--batch 8] [--steps 2048] [--checkpoints 128,256,512,1024,2048]
+                                    [--rounding counter|uniform]
 
 Runs one Mamba2 layer of Nemotron-H-8B's shape (128 heads x 64 x 128, 8 groups) for --steps
 decode steps from one initial state h0 ~ N(0, 0.5), along four paths that see identical inputs:
 
     mx4   the MX4 state, fused update with stochastic writeback (counter generator, seed 1234,
-          the reference's step offsets)                          -- lq_mx_state_update
+          the reference's step offsets; or, with --rounding uniform, a seeded uniform tensor
+          drawn per step and applied by the reference's floor(q) + (u < frac) rule)
+                                                                 -- lq_mx_state_update
     mx8   the same with the MX8 format                             -- lq_mx_state_update
     bf16  a bf16 state, fp32 update, rounded back each step        -- lq_selective_state_update
     fp32  an fp32 state                                            -- lq_selective_state_update
@@ -40,9 +43,13 @@ def _rel(a: torch.Tensor, b: torch.Tensor) -> float:
 
 
 def run(batch: int = 8, steps: int = 2048, checkpoints=(128, 256, 512, 1024, 2048),
-        seed: int = 0, device: str = "cuda:0", record: dict | None = None) -> dict:
+        seed: int = 0, device: str = "cuda:0", record: dict | None = None,
+        rounding: str = "counter") -> dict:
     """The experiment; `record`, when given, receives CPU copies of h0, A, D and every step's
-    inputs (for replaying a short chain elsewhere)."""
+    inputs (for replaying a short chain elsewhere). `rounding` is "counter" (the library's
+    generator) or "uniform" (a uniform tensor per step from the seeded generator)."""
+    if rounding not in ("counter", "uniform"):
+        raise ValueError(f"rounding must be 'counter' or 'uniform', got {rounding!r}")
     dev = torch.device(device)
     gen = torch.Generator(device=dev).manual_seed(seed)
     shape = (batch, HEADS, DIM, DSTATE)
@@ -76,12 +83,19 @@ def run(batch: int = 8, steps: int = 2048, checkpoints=(128, 256, 512, 1024, 204
                 batch, HEADS, DIM)
         Bm = torch.randn(batch, GROUPS, DSTATE, device=dev, generator=gen).to(torch.bfloat16)
         Cm = torch.randn(batch, GROUPS, DSTATE, device=dev, generator=gen).to(torch.bfloat16)
+        uni = (torch.rand(shape, device=dev, generator=gen) if rounding == "uniform" else None)
         if record is not None:
-            record["steps"].append(dict(x=x.cpu(), dt=dt.cpu(), B=Bm.cpu(), C=Cm.cpu()))
+            record["steps"].append(dict(x=x.cpu(), dt=dt.cpu(), B=Bm.cpu(), C=Cm.cpu(),
+                                        uniform=None if uni is None else uni.cpu()))
         for bits in (4, 8):
-            _abi.mx_state_update(*mx[bits], x, dt, None, A, Bm, Cm, D, None, outs[f"mx{bits}"],
-                                 bits, False, _abi.ROUND_SR_COUNTER, seed=1234,
-                                 rng_offset=(step - 1) * total)
+            if uni is None:
+                _abi.mx_state_update(*mx[bits], x, dt, None, A, Bm, Cm, D, None,
+                                     outs[f"mx{bits}"], bits, False, _abi.ROUND_SR_COUNTER,
+                                     seed=1234, rng_offset=(step - 1) * total)
+            else:
+                _abi.mx_state_update(*mx[bits], x, dt, None, A, Bm, Cm, D, None,
+                                     outs[f"mx{bits}"], bits, False, _abi.ROUND_SR_UNIFORM,
+                                     uniform=uni)
         for name, state in plain.items():
             _abi.selective_state_update(state, x, dt, None, A, Bm, Cm, D, None, outs[name], False)
         if step in marks:
@@ -102,7 +116,8 @@ def run(batch: int = 8, steps: int = 2048, checkpoints=(128, 256, 512, 1024, 204
         "steps": steps,
         "shape": list(shape),
         "groups": GROUPS,
-        "rounding": "stochastic writeback, counter generator, seed 1234",
+        "rounding": ("stochastic writeback, counter generator, seed 1234" if rounding == "counter"
+                     else "stochastic writeback, seeded uniform tensor per step (floor(q) + (u < frac))"),
         "inputs": "fresh per step: x ~ N(0,1) bf16, dt = softplus(N(0,1)) per (batch, head), "
                   "B, C ~ N(0,1) bf16; fixed A = -exp(U(0,2)), D ~ N(0,1) per head; "
                   f"h0 ~ N(0, 0.5); generator seed {seed}",
@@ -117,12 +132,13 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--checkpoints", default="128,256,512,1024,2048")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--rounding", choices=["counter", "uniform"], default="counter")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("the drift experiment needs a GPU", file=sys.stderr)
         return 1
     res = run(args.batch, args.steps, [int(c) for c in args.checkpoints.split(",") if c],
-              args.seed)
+              args.seed, rounding=args.rounding)
     print(json.dumps(res), flush=True)
     return 0
 

@@ -168,15 +168,17 @@ def test_full_size_b64_model_layout(gpu, path):
                          what=f"y batch {b}")
 
 
-def test_drift_tool_replays_on_the_oracle(gpu):
+@pytest.mark.parametrize("rounding", ["counter", "uniform"])
+def test_drift_tool_replays_on_the_oracle(gpu, rounding):
     """layer_quant_amd.drift on a short chain (batch 1, 6 steps): the reported drift of the MX4
-    state, the bf16 state and y agrees with the same chain replayed through the CPU oracle."""
+    state, the bf16 state and y agrees with the same chain replayed through the CPU oracle, with
+    the counter generator and with the supplied per-step uniform tensors."""
     import numpy as np
 
     from layer_quant_amd import drift
 
     rec = {}
-    res = drift.run(batch=1, steps=6, checkpoints=(3, 6), record=rec)
+    res = drift.run(batch=1, steps=6, checkpoints=(3, 6), record=rec, rounding=rounding)
     assert [r["step"] for r in res["drift"]] == [3, 6]
     q, e, m = omx.mx_encode(rec["h0"].numpy(), 4, omx.ROUND_NEAREST_EVEN)
     hb = rec["h0"].to(torch.bfloat16)
@@ -184,10 +186,12 @@ def test_drift_tool_replays_on_the_oracle(gpu):
     total = rec["h0"].numel()
     got = {}
     for i, s in enumerate(rec["steps"], start=1):
+        if rounding == "counter":
+            mode = dict(round_mode=omx.ROUND_SR_COUNTER, seed=1234, rng_offset=(i - 1) * total)
+        else:
+            mode = dict(round_mode=omx.ROUND_SR_UNIFORM, uniform=s["uniform"].numpy())
         q, e, m, y4, _ = omx.mx_update(q, e, m, s["x"], s["dt"], rec["A"], s["B"], s["C"],
-                                       D=rec["D"], format_bits=4,
-                                       round_mode=omx.ROUND_SR_COUNTER, seed=1234,
-                                       rng_offset=(i - 1) * total)
+                                       D=rec["D"], format_bits=4, **mode)
         hb, yb = omx.bf16_state_update(hb, s["x"], s["dt"], rec["A"], s["B"], s["C"], rec["D"])
         hf, _ = omx.update_math(hf, s["x"], s["dt"], rec["A"], s["B"], s["C"], rec["D"])
         if i in (3, 6):
