@@ -216,18 +216,19 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
 
     rows = []
     hq, hkv, d, g = 32, 8, 128, 32
-    for B in ((1, 8, 64) if which in ("all", "attention") else ()):
-        for S in (1024, 4096, 16384):
-            kp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
-            vp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
-            ks = torch.rand(B, hkv, S, d // g, device=dev, generator=gen) + 0.01
-            vs = torch.rand(B, hkv, S, d // g, device=dev, generator=gen) + 0.01
-            q = torch.randn(B, hq, 1, d, device=dev, generator=gen).to(torch.bfloat16)
-            out = torch.empty(B, hq, d, device=dev, dtype=torch.bfloat16)
-            med, mean = timed(lambda: _abi.int4_decode_attention(q, kp, vp, ks, vs, None, out, S, 4, g))
-            rows.append(row("int4_decode_attention", attention_bytes(B, hq, hkv, d, S, g), med, mean,
-                            batch=B, ctx=S, group=g))
-            del kp, vp, ks, vs
+    shapes = [(B, S, g) for B in (1, 8, 64) for S in (1024, 4096, 16384)]
+    shapes.append((8, 2072, 64))  # the shape of the reference's own published figure (A100)
+    for B, S, gs in (shapes if which in ("all", "attention") else ()):
+        kp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
+        vp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
+        ks = torch.rand(B, hkv, S, d // gs, device=dev, generator=gen) + 0.01
+        vs = torch.rand(B, hkv, S, d // gs, device=dev, generator=gen) + 0.01
+        q = torch.randn(B, hq, 1, d, device=dev, generator=gen).to(torch.bfloat16)
+        out = torch.empty(B, hq, d, device=dev, dtype=torch.bfloat16)
+        med, mean = timed(lambda: _abi.int4_decode_attention(q, kp, vp, ks, vs, None, out, S, 4, gs))
+        rows.append(row("int4_decode_attention", attention_bytes(B, hq, hkv, d, S, gs), med, mean,
+                        batch=B, ctx=S, group=gs))
+        del kp, vp, ks, vs
     nh, p_, n, ng = 128, 64, 128, 8
     for B in ((1, 8, 64) if which in ("all", "state") else ()):
         x = torch.randn(B, nh, p_, device=dev, generator=gen).to(torch.bfloat16)
