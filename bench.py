@@ -295,6 +295,43 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
             "write-back would compete with the timed kernel)", "peak_GB_s": PEAK_HBM_GBS}
 
 
+def config1_gpu(torch, dev, reps: int = 20) -> float:
+    """BASELINE config 1 on the GPU through the C ABI: pack a 1024-token K/V cache (two
+    lq_int4_pack_kv calls) and attend once (lq_int4_decode_attention), batch 1, 32 q / 8 KV
+    heads, group 32; median us per repetition (HIP events)."""
+    from layer_quant_amd import _abi
+
+    hq, hkv, d, g, S = 32, 8, 128, 32, 1024
+    gen = torch.Generator(device=dev).manual_seed(0)
+    k = torch.randn(1, hkv, S, d, device=dev, generator=gen).to(torch.bfloat16)
+    v = torch.randn(1, hkv, S, d, device=dev, generator=gen).to(torch.bfloat16)
+    q = torch.randn(1, hq, 1, d, device=dev, generator=gen).to(torch.bfloat16)
+    kp = torch.empty(1, hkv, S, d // 2, dtype=torch.uint8, device=dev)
+    vp = torch.empty_like(kp)
+    ks = torch.empty(1, hkv, S, d // g, device=dev)
+    vs = torch.empty_like(ks)
+    pos = torch.arange(S, device=dev)
+    out = torch.empty(1, hq, d, device=dev, dtype=torch.bfloat16)
+
+    def once():
+        _abi.int4_pack_kv(k, kp, ks, pos, g)
+        _abi.int4_pack_kv(v, vp, vs, pos, g)
+        _abi.int4_decode_attention(q, kp, vp, ks, vs, None, out, S, hq // hkv, g)
+
+    once()
+    ts = []
+    for _ in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        once()
+        b.record()
+        ts.append((a, b))
+    torch.cuda.synchronize()
+    us = sorted(1000.0 * a.elapsed_time(b) for a, b in ts)
+    return us[len(us) // 2]
+
+
 def cpu_baseline(args):
     """The CPU oracle (torch fp32/fp64 restatement of the reference formulas) on a bounded
     sample of the same step, on this host's cores, scaled linearly to the full step."""
@@ -345,7 +382,20 @@ def cpu_baseline(args):
             ts.append(time.perf_counter() - t0)
         return float(np.median(ts))
 
+    # BASELINE config 1 (the reference's CPU-runnable case): pack a 1024-token K/V cache and
+    # attend once, batch 1, 32 q / 8 KV heads, group 32, seed 0
+    g1 = 32
+    kv1 = torch.randn(2, 1, hkv, 1024, d, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    q1 = torch.randn(1, hq, 1, d, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+
+    def config1_once():
+        c1 = oik.allocate_cache(1, hkv, 1024, d, g1)
+        oik.pack_kv_into_cache(c1, kv1[0], kv1[1], torch.arange(1024), g1)
+        oik.decode_attention(q1, c1["k_packed"], c1["v_packed"], c1["k_scale"], c1["v_scale"],
+                             1024, 4, g1)
+
     reps = 3
+    t_cfg1 = timed(config1_once, 5)
     t_attn = timed(attn_once, reps)
     t_mx = timed(mx_once, reps)
     scale_attn = (args.batch / ba_sample) * (args.ctx / s_sample)
@@ -363,6 +413,7 @@ def cpu_baseline(args):
                    f"layers x batch {args.batch} x ctx {args.ctx} and {args.mamba_layers} layers x "
                    f"batch {args.batch}; attention {t_attn * 1e3:.1f} ms, update "
                    f"{t_mx * 1e3:.1f} ms per sample call"),
+        "config1_us": round(t_cfg1 * 1e6, 1),
     }
 
 
@@ -451,10 +502,17 @@ def main():
         "frac": dk["frac_of_peak"],
         "traffic": load_traffic(dominant, workload),
     }
+    cfg1_gpu = config1_gpu(torch, dev)
     cpu = None
+    cfg1 = None
     if args.cpu_baseline == "on":
         log("cpu baseline")
         cpu = cpu_baseline(args)
+        cfg1_cpu = cpu.pop("config1_us")
+        cfg1 = {"workload": "BASELINE config 1: pack a 1024-token INT4 K/V cache + one q_len=1 "
+                            "decode attention, batch 1, 32 q / 8 KV heads, head_dim 128, group 32",
+                "gpu_us": round(cfg1_gpu, 1), "cpu_us": cfg1_cpu, "cpu_cores": cpu["cores"],
+                "cpu_kind": "port (oracle)"}
     line = {
         "metric": METRIC,
         "value": round(step_s * 1e6, 1),
@@ -484,6 +542,7 @@ def main():
         "kernels": kernels,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "config1_cpu_vs_gpu": cfg1,
     }
     print(json.dumps(line), flush=True)
 
