@@ -77,17 +77,21 @@ __device__ __forceinline__ u32x4_t decode_k(uint32_t w) {
   return o;
 }
 
-// sum over the columns that share a query head: columns j = m*NREP + h, unused columns hold 0
+// a * b summed over the columns that share a query head: columns j = m*NREP + h, unused columns
+// hold 0. Row rotations by 8, 4, 2, 1 lanes; with contraction off each level is one
+// v_add_f32_dpp (a fused multiply-add cannot take the DPP operand and would need a separate move).
 template <int NREP>
-__device__ __forceinline__ float column_sum(float x) {
+__device__ __forceinline__ float column_sum(float a, float b) {
+#pragma clang fp contract(off)
+  float x = a * b;
   if constexpr (NREP <= 8) x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+                                0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, true));
   if constexpr (NREP <= 4) x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                0, __builtin_bit_cast(int, x), 0x124, 0xf, 0xf, false));
+                                0, __builtin_bit_cast(int, x), 0x124, 0xf, 0xf, true));
   if constexpr (NREP <= 2) x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                0, __builtin_bit_cast(int, x), 0x122, 0xf, 0xf, false));
+                                0, __builtin_bit_cast(int, x), 0x122, 0xf, 0xf, true));
   if constexpr (NREP <= 1) x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                0, __builtin_bit_cast(int, x), 0x121, 0xf, 0xf, false));
+                                0, __builtin_bit_cast(int, x), 0x121, 0xf, 0xf, true));
   return x;
 }
 
@@ -277,7 +281,7 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
         const f32x4_t ks4 = *(const f32x4_t*)&sc_lds[wave][buf][0][colm][SUB * sb + 16 * t + 4 * q4];
         vsc[sb][t] = *(const f32x4_t*)&sc_lds[wave][buf][1][colm][SUB * sb + 16 * t + 4 * q4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s[sb][4 * t + r] = column_sum<NREP>(sacc[sb][t][r] * ks4[r]);
+        for (int r = 0; r < 4; ++r) s[sb][4 * t + r] = column_sum<NREP>(sacc[sb][t][r], ks4[r]);
       }
     }
     if (p.mask != nullptr) {
@@ -324,12 +328,15 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
       }
       m_run = m_new;
     }
+    // m_run is -inf only while every score so far is -inf; a finite stand-in keeps
+    // exp2(-inf - m) = 0 without a per-score select (a finite score takes the update above)
+    const float m_use = fmaxf(m_run, -3.0e38f);
     float psum = 0.0f;
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        s[sb][e] = (s[sb][e] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[sb][e] - m_run);
+        s[sb][e] = __builtin_amdgcn_exp2f(s[sb][e] - m_use);
         psum += s[sb][e];
       }
     }
