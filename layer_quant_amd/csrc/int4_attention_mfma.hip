@@ -5,26 +5,30 @@
 // Every packed KV byte and scale is read from HBM once per (batch, KV head): the NREP query
 // heads that share a KV head are columns of the same MFMA tile.
 //
+// Streaming. Each wave keeps a ring of 3 tile buffers in LDS filled by buffer loads that write
+// LDS directly (16 bytes per lane, non-temporal): while tile i is computed, the loads of tiles
+// i+1 and i+2 are in flight, with no registers held for them. This replaced a ring of register
+// tiles (3 x 24 VGPRs per lane, V passed through LDS for its transpose anyway).
+//
 // MFMA v_mfma_f32_16x16x32_bf16, D[16x16] += A[16x32] * B[32x16]. Lane l holds A row l%16 and
 // B column l%16, each with K slots 8*(l/16) .. +7, and D rows 4*(l/16) .. +3 of column l%16.
 //
 // Columns. The 16 columns are (group m, head h) pairs, j = m*NREP + h, NREP*(128/g) <= 16.
 //
-// QK^T. Lane (q, r) loads the 16-byte unit q (dims 32q .. 32q+31) of key row r with one dwordx4
-// and feeds dword c of it to MFMA c (A = 16 keys x 32 K slots). B = the matching query dims,
+// QK^T. Lane (q, r) reads the 16-byte unit q (dims 32q .. 32q+31) of key row r from LDS and
+// feeds dword c of it to MFMA c (A = 16 keys x 32 K slots). B = the matching query dims,
 // placed only in the columns whose group m owns them (zero elsewhere), so after the 4 MFMAs
 // column (m, h) holds the group-m partial dot product of head h; scaling by the key scale of
 // group m and summing the columns of equal h (DPP row rotations) gives the score of head h.
 // Nibbles decode in registers to bf16 with a magic number: bits 0x4300 | (n ^ 8) are the value
-// 136 + n, so the accumulator starts at -136 * sum(q) of the column's dims.
+// 136 + n, so the accumulator starts at -136 * sum(q) of the column's dims. Scores stay in raw
+// units; log2(e)/sqrt(D) is applied inside the exponent's fused multiply-add.
 //
 // P V. A = V^T: 16 dims x 32 keys, B = P' with P'[key][(m, h)] = p[key][h] * vscale[key][m].
-// Lane (q, c) needs dword c of key rows q + 4e (e = 0..7), so MFMA k (k = 0..7) covers dims
-// 8c + k. The V rows arrive as 128-bit loads (32-bit loads cap the stream near 4.2 TB/s on MI355X
-// against 7 TB/s for 128-bit) and pass through a per-wave LDS buffer into that layout; the output
-// column (m, h) is kept only for dims of group m. P' is split into bf16 hi + lo (two MFMAs, about
-// 16 significant bits). The value offset 136 of the V decode is removed at the end with
-// sum_keys P' from one more MFMA against a ones operand.
+// Lane (q, c) reads dword c of key rows q + 4e (e = 0..7) from LDS, so MFMA k (k = 0..7) covers
+// dims 8c + k; the output column (m, h) is kept only for dims of group m. P' is split into bf16
+// hi + lo (two MFMAs, about 16 significant bits). The value offset 136 of the V decode is removed
+// at the end with sum_keys P' from one more MFMA against a ones operand.
 #include <math.h>
 #include <stdlib.h>
 
@@ -43,14 +47,15 @@ constexpr int FAST_D = 128;
 constexpr int SUB = 32;              // keys per MFMA sub-tile (the K depth of the P V product)
 constexpr int NSUB = 1;              // sub-tiles per iteration; one softmax max per iteration
 constexpr int TILE = SUB * NSUB;     // keys per wave iteration
-constexpr int WAVES = 4;
+constexpr int WAVES = 4;             // waves per workgroup, each on its own key range
+constexpr int THREADS = 64 * WAVES;
+constexpr int NBUF = 3;              // LDS tile buffers per wave (3 or 4; 4 measured no faster)
 constexpr float LAZY_LOG2 = 8.0f;    // running-max slack of the lazy softmax rescale
 constexpr uint32_t NIB2 = 0x000F000Fu;
 constexpr int BUF_DWORD3 = 0x00020000;  // raw 32-bit buffer, gfx9 family
-// Non-temporal (streaming) loads of the packed K/V rows and scales: each byte is read once per
-// call, and at B=64, ctx 16384 the 1.34 GB stream measured 248 us with the default policy and
-// 237 us with nt (a read-only probe of the same volume: 7.2 TB/s with nt, 5.4-6.3 without).
-constexpr int KV_LOAD_POLICY = 2;
+// The tile loads carry the non-temporal (nt) policy: each byte is read once per call, and at
+// B=64, ctx 16384 the 1.34 GB stream measured 248 us with the default policy and 237 us with nt
+// (a read-only probe of the same volume: 7.2 TB/s with nt, 5.4-6.3 without).
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) {
   return __builtin_bit_cast(bf16x8_t, v);
@@ -95,30 +100,70 @@ __device__ __forceinline__ float column_sum(float a, float b) {
   return x;
 }
 
-template <int G>
-struct TileRegs {
-  u32x4_t kq[NSUB][2];      // [sub][16-key half]: 16-byte unit l/16 (dims 32*(l/16) ..) of row l%16
-  u32x4_t vq[NSUB][2];      // [sub][16-key half]: 16-byte unit l%4 of V row l/4
-  float ksr[G];             // key / value scales of key row l%32, staged through LDS
-  float vsr[G];
+// One wave's copy of a 32-key tile in LDS, written by buffer loads that deliver straight to LDS
+// (16 bytes per lane: lane l of one load writes bytes 16 l .. 16 l + 15 of its 1 KiB destination).
+// K rows: 16-byte unit q of row r (r = key & 15 of the half) sits in slot 4 r + (q ^ ((r >> 2) & 3)),
+// so that the 16 lanes of one row group of the QK reads hit 16 different slots modulo 16.
+// V rows and the scales keep their HBM order ([key][64 bytes], [key][group]).
+struct alignas(16) TileLds {
+  u32x4_t k[2][64];
+  u32x4_t v[2][64];
+  float ks[TILE * 4];  // [key][group] (G <= 4)
+  float vs[TILE * 4];
 };
 
-// G consecutive fp32 scale words at byte offset off, as one buffer load. (The words are
-// reinterpreted with __uint_as_float: with this compiler, __builtin_bit_cast(float, w[m]) of a
-// vector element narrowed the 128-bit load to its first dword and lost the other three.)
-template <int G>
-__device__ __forceinline__ void load_scales(__amdgpu_buffer_rsrc_t r, int off, float (&v)[G]) {
-  if constexpr (G == 4) {
-    const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, KV_LOAD_POLICY);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) v[m] = __uint_as_float(w[m]);
-  } else if constexpr (G == 2) {
-    const u32x2_t w = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, KV_LOAD_POLICY);
-    v[0] = __uint_as_float(w[0]);
-    v[1] = __uint_as_float(w[1]);
-  } else {
-    v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, KV_LOAD_POLICY));
-  }
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor (base, stride 0, num_records = bytes, gfx9 dword 3) for wave-uniform
+// arguments, so that it lives in 4 SGPRs.
+__device__ __forceinline__ i32x4_t make_desc(const void* base, int bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  i32x4_t d;
+  d[0] = (int32_t)(uint32_t)a;
+  d[1] = (int32_t)((uint32_t)(a >> 32) & 0xffffu);
+  d[2] = bytes;
+  d[3] = BUF_DWORD3;
+  return d;
+}
+
+// One 16-byte-per-lane buffer load that writes LDS directly: lane l's 16 bytes (at byte offset
+// voff of the buffer; zero past num_records) land at LDS byte address lds + 16 l. Written as
+// inline assembly with its own M0 set-up: the compiler's wait insertion for the builtin form did
+// not track which LDS buffer each such load targets (it emitted no wait before the reads of one
+// buffer and a full wait before the other's), so the waits are explicit (wait_loads) instead.
+// M0 is declared clobbered; no other code of this kernel uses M0 (the compiler warns that a
+// reserved register in a clobber list is not saved for it).
+__device__ __forceinline__ void load_to_lds(i32x4_t desc, const void* lds, int voff) {
+  const uint32_t addr =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen nt lds"
+      :
+      : "s"(addr), "v"(voff), "s"(desc)
+      : "memory", "m0");
+}
+
+// The same with 4 bytes per lane (lane l's dword lands at lds + 4 l; each dword is range-checked
+// on its own).
+__device__ __forceinline__ void load_to_lds_b32(i32x4_t desc, const void* lds, int voff) {
+  const uint32_t addr =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %1, %2, 0 offen nt lds"
+      :
+      : "s"(addr), "v"(voff), "s"(desc)
+      : "memory", "m0");
+}
+
+// Wait until at most N vector-memory loads of this wave are outstanding (loads complete in issue
+// order, so every load older than the newest N has landed).
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
 // Per-wave bases of this (batch, KV head) block; rows are contiguous (64 packed bytes, G scale
@@ -130,44 +175,55 @@ struct Rsrc {
   const uint8_t* vb;
   const float* ksb;
   const float* vsb;
-  int kvo, vvo, svo;  // per-lane byte offsets inside a tile (K unit, V unit, scale row)
+  int kvo;  // this lane's source offset for the swizzled K slot
 };
 
+// Issue the 6 loads of the tile at key tb into B (2 for K, 2 for V, one each for the K and V
+// scales on lanes below 8 G).
 template <int G>
-__device__ __forceinline__ void load_tile(const Rsrc& R, int tb, int S, TileRegs<G>& r) {
-  tb = __builtin_amdgcn_readfirstlane(tb);  // uniform by construction; lets the descriptors live in SGPRs
+__device__ __forceinline__ void issue_tile(const Rsrc& R, int tb, int S, TileLds& B, int lane) {
+  tb = __builtin_amdgcn_readfirstlane(tb);  // uniform by construction; descriptors in SGPRs
   const int rem = S - tb;  // > 0
-  const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(R.kb + (int64_t)tb * 64), 0, rem * 64, BUF_DWORD3);
-  const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(R.vb + (int64_t)tb * 64), 0, rem * 64, BUF_DWORD3);
-  const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(R.ksb + (int64_t)tb * G), 0, rem * G * 4, BUF_DWORD3);
-  const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(R.vsb + (int64_t)tb * G), 0, rem * G * 4, BUF_DWORD3);
-  load_scales<G>(rks, R.svo, r.ksr);  // lanes l and l + 32 read the same row
-  load_scales<G>(rvs, R.svo, r.vsr);
+  const i32x4_t rk = make_desc(R.kb + (int64_t)tb * 64, rem * 64);
+  const i32x4_t rv = make_desc(R.vb + (int64_t)tb * 64, rem * 64);
 #pragma unroll
-  for (int sb = 0; sb < NSUB; ++sb) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      r.kq[sb][t] = __builtin_bit_cast(
-          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, R.kvo + (SUB * sb + 16 * t) * 64, 0, KV_LOAD_POLICY));
-      r.vq[sb][t] = __builtin_bit_cast(
-          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, R.vvo + (SUB * sb + 16 * t) * 64, 0, KV_LOAD_POLICY));
+  for (int h = 0; h < 2; ++h) {
+    load_to_lds(rk, &B.k[h][0], R.kvo + 1024 * h);
+    load_to_lds(rv, &B.v[h][0], 16 * lane + 1024 * h);
+  }
+  const i32x4_t rks = make_desc(R.ksb + (int64_t)tb * G, rem * G * 4);
+  const i32x4_t rvs = make_desc(R.vsb + (int64_t)tb * G, rem * G * 4);
+  // the tile's 32 G scale words of each kind: 16 bytes per lane on lanes 0..31 for G = 4, one
+  // dword per lane on lanes below 32 G otherwise (16-byte units would straddle the end of the
+  // scales at a ragged S); the other lanes are inactive and write nothing
+  if constexpr (G == 4) {
+    if (lane < 32) {
+      load_to_lds(rks, &B.ks[0], 16 * lane);
+      load_to_lds(rvs, &B.vs[0], 16 * lane);
+    }
+  } else {
+    if (lane < 32 * G) {
+      load_to_lds_b32(rks, &B.ks[0], 4 * lane);
+      load_to_lds_b32(rvs, &B.vs[0], 4 * lane);
     }
   }
 }
 
 template <int NREP, int G>
-__global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
+__global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   constexpr int NCOL = NREP * G;
   constexpr int CPG = 4 / G;  // 32-dim chunks per group
   static_assert(NCOL <= 16, "columns exceed the MFMA tile");
-  __shared__ float sc_lds[WAVES][2][2][G][TILE];  // [wave][buffer][k/v][group][key]
-  __shared__ u32x4_t v_lds[WAVES][TILE][4];         // [wave][key][16-byte unit]: one V tile
-  __shared__ float o_lds[WAVES][NREP][FAST_D];
-  __shared__ float ml_lds[WAVES][2][NREP];
+  static_assert(NSUB == 1, "one 32-key sub-tile per tile");
+  static_assert(NBUF == 3 || NBUF == 4, "3 or 4 tile buffers");
+  // NBUF tile buffers per wave (separate LDS objects, one per ring position); a wave's partial
+  // output and softmax state reuse its first buffer when they fit (NREP <= 8)
+  constexpr bool O_IN_TILE = (NREP * FAST_D + 2 * NREP) * 4 <= (int)sizeof(TileLds);
+  __shared__ TileLds tiles0[WAVES];
+  __shared__ TileLds tiles1[WAVES];
+  __shared__ TileLds tiles2[WAVES];
+  __shared__ TileLds tiles3[NBUF > 3 ? WAVES : 1];
+  __shared__ float o_sep[O_IN_TILE ? 1 : WAVES * (NREP * FAST_D + 2 * NREP)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -188,6 +244,19 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
   const bool colvalid = c16 < NCOL;
   const int colh = c16 % NREP;
   const int colm = colvalid ? c16 / NREP : 0;
+
+  Rsrc R;
+  R.kb = p.kp + b * p.kps[0] + kvh * p.kps[1];
+  R.vb = p.vp + b * p.vps[0] + kvh * p.vps[1];
+  R.ksb = p.ks + b * p.kss[0] + kvh * p.kss[1];
+  R.vsb = p.vs + b * p.vss[0] + kvh * p.vss[1];
+  // K slot l of a half holds row l >> 2, unit (l & 3) ^ ((l >> 4) & 3)
+  R.kvo = (lane >> 2) * 64 + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
+
+  // the first tiles' loads go out before the query set-up
+  if (w0 < w1) issue_tile<G>(R, w0, S, tiles0[wave], lane);
+  if (w0 + TILE < w1) issue_tile<G>(R, w0 + TILE, S, tiles1[wave], lane);
+  if (NBUF > 3 && w0 + 2 * TILE < w1) issue_tile<G>(R, w0 + 2 * TILE, S, tiles2[wave], lane);
 
   // Query operands. Lane (q, .) feeds MFMA c with dword c of its key unit q, i.e. dims
   // 32q + 8c .. 32q + 8c + 7 (slot order kPerm); the query is placed only in the columns whose
@@ -214,18 +283,13 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
   qsum += __shfl_xor(qsum, 16, 64);
   qsum += __shfl_xor(qsum, 32, 64);
   const float cinit = -136.0f * qsum;
+  const float csm = p.scale_sm;  // raw scores -> log2 units
+  const float inv_csm = 1.0f / csm;
 
-  Rsrc R;
-  R.kb = p.kp + b * p.kps[0] + kvh * p.kps[1];
-  R.vb = p.vp + b * p.vps[0] + kvh * p.vps[1];
-  R.ksb = p.ks + b * p.kss[0] + kvh * p.kss[1];
-  R.vsb = p.vs + b * p.vss[0] + kvh * p.vss[1];
   // QK A-row i of a 16-key half is key 4 (i & 3) + (i >> 2), so that output row 4q + r (held by
-  // lane group q) is key 4r + q, and lane group q's 8 keys of a 32-key sub-tile are q + 4e
-  // (e = 4t + r): the V loads of key slot e then cover keys 4e .. 4e+3 contiguously.
-  R.kvo = (4 * (c16 & 3) + (c16 >> 2)) * 64 + 16 * q4;
-  R.vvo = (lane >> 2) * 64 + 16 * (lane & 3);
-  R.svo = (lane & 31) * G * 4;
+  // lane group q) is key 4r + q, and lane group q's 8 keys of the tile are q + 4e (e = 4t + r).
+  const int krow = 4 * (c16 & 3) + (c16 >> 2);
+  const int kslot = 4 * krow + (q4 ^ (c16 & 3));
 
   float m_run = -INFINITY;
   float l_run = 0.0f;
@@ -235,85 +299,85 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
   f32x4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
   const u32x4_t ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
 
-  // Scales of a tile go to LDS, transposed to [group][key] with log2(e)/sqrt(D) folded into the
-  // key scales, one tile before their use; buffer (tile index & 1).
-  auto stage_scales = [&](const TileRegs<G>& r, const int buf) {
-    if (lane < TILE) {
-      const int tok = lane;
-      // key 16t + 4r + q is read by lane group q as element r: store it at 16t + 4q + r
-      const int pos = (tok & ~15) | ((tok & 3) << 2) | ((tok >> 2) & 3);
-#pragma unroll
-      for (int m = 0; m < G; ++m) {
-        sc_lds[wave][buf][0][m][pos] = r.ksr[m] * p.scale_sm;
-        sc_lds[wave][buf][1][m][pos] = r.vsr[m];
-      }
-    }
+  // Before tile tb's reads: wait for its 6 loads, leaving the already issued loads of the
+  // following tiles (6 each) in flight.
+  auto wait_tile = [&](const int tb) {
+    if (NBUF > 3 && tb + 3 * TILE < w1) wait_loads<18>();
+    else if (tb + 2 * TILE < w1) wait_loads<12>();
+    else if (tb + TILE < w1) wait_loads<6>();
+    else wait_loads<0>();
   };
 
-  auto process = [&](const int tb, const TileRegs<G>& cur, const TileRegs<G>& next,
-                     const bool has_next) {
-    const int buf = ((tb - w0) / TILE) & 1;
-    if (has_next) stage_scales(next, buf ^ 1);
-    // scores: per sub-tile 2 halves of 16 keys, 4 chunks each
-    f32x4_t sacc[NSUB][2];
+  auto process = [&](const int tb, const TileLds& B) {
+    wait_tile(tb);
+    // scores S^T (keys x columns) in raw units: two 16-key halves, 4 chunks each
+    f32x4_t sacc[2];
+    sacc[0] = f32x4_t{cinit, cinit, cinit, cinit};
+    sacc[1] = sacc[0];
+    u32x4_t kq[2];
 #pragma unroll
-    for (int sb = 0; sb < NSUB; ++sb) {
-      sacc[sb][0] = f32x4_t{cinit, cinit, cinit, cinit};
-      sacc[sb][1] = sacc[sb][0];
-      // the two 16-key halves are independent chains: interleave them
+    for (int t = 0; t < 2; ++t) kq[t] = B.k[t][kslot];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < 4; ++c) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          sacc[sb][t] = mfma_bf16(decode_k(cur.kq[sb][t][c]), qop[c], sacc[sb][t]);
+      for (int t = 0; t < 2; ++t) sacc[t] = mfma_bf16(decode_k(kq[t][c]), qop[c], sacc[t]);
+    }
+    // V operands, decoded here (they do not depend on the scores) so that this VALU work shares
+    // a basic block with the QK MFMAs above: dword c16 of key rows q4 + 4e (e = 0..7), key slots
+    // (2u, 2u+1) paired, nibble k of each dword -> MFMA k
+    u32x4_t va[8];
+    {
+      const uint32_t* vrow = (const uint32_t*)&B.v[0][0];
+      uint32_t vw[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vw[e] = vrow[(q4 + 4 * e) * 16 + c16];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t ylo = __builtin_amdgcn_perm(vw[2 * u + 1], vw[2 * u], 0x05040100u);
+        const uint32_t yhi = __builtin_amdgcn_perm(vw[2 * u + 1], vw[2 * u], 0x07060302u);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          va[j][u] = nib_pair(ylo >> (4 * j));
+          va[4 + j][u] = nib_pair(yhi >> (4 * j));
         }
       }
+      // keep the decode here: without this the compiler sinks it past the softmax branches to
+      // its use in the P V products
+#pragma unroll
+      for (int k = 0; k < 8; ++k) asm volatile("" : "+v"(va[k]));
     }
-    __builtin_amdgcn_wave_barrier();
 
-    // key slot e of sub-tile sb (e = 4t + r) is key tb + 32 sb + 16 t + 4 r + (l/16)
-    float s[NSUB][8];
-    f32x4_t vsc[NSUB][2];
+    // key slot e (e = 4t + r) is key tb + 16 t + 4 r + (l/16)
+    float s[8], vsc[8];
 #pragma unroll
-    for (int sb = 0; sb < NSUB; ++sb) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const f32x4_t ks4 = *(const f32x4_t*)&sc_lds[wave][buf][0][colm][SUB * sb + 16 * t + 4 * q4];
-        vsc[sb][t] = *(const f32x4_t*)&sc_lds[wave][buf][1][colm][SUB * sb + 16 * t + 4 * q4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s[sb][4 * t + r] = column_sum<NREP>(sacc[sb][t][r], ks4[r]);
-      }
+    for (int e = 0; e < 8; ++e) {
+      const int key = 16 * (e >> 2) + 4 * (e & 3) + q4;
+      s[e] = column_sum<NREP>(sacc[e >> 2][e & 3], B.ks[key * G + colm]);
+      vsc[e] = B.vs[key * G + colm];
     }
     if (p.mask != nullptr) {
 #pragma unroll
-      for (int sb = 0; sb < NSUB; ++sb) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int tok = tb + SUB * sb + 16 * (e >> 2) + 4 * (e & 3) + q4;
-          s[sb][e] += (tok < p.mask_len) ? p.mask[b * p.mask_sb + (int64_t)tok * p.mask_sk]
-                                         : -INFINITY;
-        }
+      for (int e = 0; e < 8; ++e) {
+        const int tok = tb + 16 * (e >> 2) + 4 * (e & 3) + q4;
+        s[e] += (tok < p.mask_len) ? p.mask[b * p.mask_sb + (int64_t)tok * p.mask_sk] * inv_csm
+                                   : -INFINITY;
       }
     }
-    if (tb + TILE > w1) {
+    if (tb + TILE > w1) {  // keys past this wave's range: no score, no value scale
 #pragma unroll
-      for (int sb = 0; sb < NSUB; ++sb) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int tok = tb + SUB * sb + 16 * (e >> 2) + 4 * (e & 3) + q4;
-          s[sb][e] = tok < w1 ? s[sb][e] : -INFINITY;
-        }
+      for (int e = 0; e < 8; ++e) {
+        const int tok = tb + 16 * (e >> 2) + 4 * (e & 3) + q4;
+        s[e] = tok < w1 ? s[e] : -INFINITY;
+        vsc[e] = tok < w1 ? vsc[e] : 0.0f;
       }
     }
-    // Lazy rescaling: p = 2^(s - m_run) with a running max that only moves when a score exceeds
-    // it by more than LAZY_LOG2 (p <= 2^LAZY_LOG2 otherwise), so the cross-lane max and the
-    // accumulator rescale leave the common path. The first tile always takes the update.
+    // Lazy rescaling: p = 2^(csm s - m_run) with a running max that only moves when a score
+    // exceeds it by more than LAZY_LOG2 (p <= 2^LAZY_LOG2 otherwise), so the cross-lane max and
+    // the accumulator rescale leave the common path. The first tile always takes the update.
     float lm = -INFINITY;
 #pragma unroll
-    for (int sb = 0; sb < NSUB; ++sb) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lm = fmaxf(lm, s[sb][e]);
-    }
+    for (int e = 0; e < 8; ++e) lm = fmaxf(lm, s[e]);
+    lm *= csm;
     if (__any(lm > m_run + LAZY_LOG2)) {
       float mt = fmaxf(lm, __shfl_xor(lm, 16, 64));
       mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
@@ -333,118 +397,108 @@ __global__ __launch_bounds__(256) void attn_fast_kernel(AttnParams p) {
     const float m_use = fmaxf(m_run, -3.0e38f);
     float psum = 0.0f;
 #pragma unroll
-    for (int sb = 0; sb < NSUB; ++sb) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        s[sb][e] = __builtin_amdgcn_exp2f(s[sb][e] - m_use);
-        psum += s[sb][e];
-      }
+    for (int e = 0; e < 8; ++e) {
+      s[e] = __builtin_amdgcn_exp2f(fmaf(s[e], csm, -m_use));
+      psum += s[e];
     }
     l_run += psum;
 
+    // P' = p * vscale, split into bf16 hi + lo
+    u32x4_t bhi, blo;
 #pragma unroll
-    for (int sb = 0; sb < NSUB; ++sb) {
-      // P' = p * vscale, split into bf16 hi + lo
-      u32x4_t bhi, blo;
+    for (int u = 0; u < 4; ++u) {
+      const float a0 = s[2 * u] * vsc[2 * u];
+      const float a1 = s[2 * u + 1] * vsc[2 * u + 1];
+      const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a0, a1}, bf16x2_t));
+      const float r0 = a0 - __builtin_bit_cast(float, h << 16);
+      const float r1 = a1 - __builtin_bit_cast(float, h & 0xffff0000u);
+      bhi[u] = h;
+      blo[u] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t));
+    }
+    // hi products of four dims-sets, then their lo products, so that the two MFMAs into one
+    // accumulator are separated by three independent ones
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int e = 2 * u;
-        const float a0 = s[sb][e] * vsc[sb][e >> 2][e & 3];
-        const float a1 = s[sb][e + 1] * vsc[sb][(e + 1) >> 2][(e + 1) & 3];
-        const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a0, a1}, bf16x2_t));
-        const float r0 = a0 - __builtin_bit_cast(float, h << 16);
-        const float r1 = a1 - __builtin_bit_cast(float, h & 0xffff0000u);
-        bhi[u] = h;
-        blo[u] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t));
-      }
-      // V rows through this wave's LDS buffer: dword c16 of key rows q4 + 4e (e = 0..7)
+    for (int k0 = 0; k0 < 8; k0 += 4) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) v_lds[wave][16 * t + (lane >> 2)][lane & 3] = cur.vq[sb][t];
-      const uint32_t* vrow = (const uint32_t*)&v_lds[wave][0][0];
-      uint32_t vw[8];
+      for (int j = 0; j < 4; ++j) acc[k0 + j] = mfma_bf16(va[k0 + j], bhi, acc[k0 + j]);
+      if (k0 == 0) corr = mfma_bf16(ones, bhi, corr);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vw[e] = vrow[(q4 + 4 * e) * 16 + c16];
-      // V decode: pair the key slots (2u, 2u+1), nibble k of each dword -> MFMA k
-      uint32_t ylo[4], yhi[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        ylo[u] = __builtin_amdgcn_perm(vw[2 * u + 1], vw[2 * u], 0x05040100u);
-        yhi[u] = __builtin_amdgcn_perm(vw[2 * u + 1], vw[2 * u], 0x07060302u);
-      }
-      // four dims-sets at a time: their hi products, then their lo products, so that the two
-      // MFMAs into one accumulator are separated by three independent ones
-#pragma unroll
-      for (int k0 = 0; k0 < 8; k0 += 4) {
-        u32x4_t a[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) a[j][u] = nib_pair((k0 < 4 ? ylo[u] : yhi[u]) >> (4 * j));
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[k0 + j] = mfma_bf16(a[j], bhi, acc[k0 + j]);
-        if (k0 == 0) corr = mfma_bf16(ones, bhi, corr);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[k0 + j] = mfma_bf16(a[j], blo, acc[k0 + j]);
-        if (k0 == 4) corr = mfma_bf16(ones, blo, corr);
-      }
+      for (int j = 0; j < 4; ++j) acc[k0 + j] = mfma_bf16(va[k0 + j], blo, acc[k0 + j]);
+      if (k0 == 4) corr = mfma_bf16(ones, blo, corr);
     }
     __builtin_amdgcn_wave_barrier();
   };
 
-  // three register stages: two tiles of loads stay in flight while a third is processed (a
-  // fourth stage measured the same)
-  TileRegs<G> ra, rb, rc;
-  if (w0 < w1) {
-    load_tile<G>(R, w0, S, ra);
-    stage_scales(ra, 0);
-  }
-  if (w0 + TILE < w1) load_tile<G>(R, w0 + TILE, S, rb);
-  for (int tb = w0; tb < w1; tb += 3 * TILE) {
-    if (tb + 2 * TILE < w1) load_tile<G>(R, tb + 2 * TILE, S, rc);
-    process(tb, ra, rb, tb + TILE < w1);
-    if (tb + TILE >= w1) break;
-    if (tb + 3 * TILE < w1) load_tile<G>(R, tb + 3 * TILE, S, ra);
-    process(tb + TILE, rb, rc, tb + 2 * TILE < w1);
-    if (tb + 2 * TILE >= w1) break;
-    if (tb + 4 * TILE < w1) load_tile<G>(R, tb + 4 * TILE, S, rb);
-    process(tb + 2 * TILE, rc, ra, tb + 3 * TILE < w1);
+  // NBUF-deep ring of LDS tiles: the loads of the next NBUF - 1 tiles are in flight while one
+  // is processed (the loop is unrolled by NBUF so that each buffer is a distinct LDS object and
+  // the compiler's wait before a buffer's reads counts only that buffer's loads)
+  if constexpr (NBUF > 3) {
+    for (int tb = w0; tb < w1; tb += 4 * TILE) {
+      if (tb + 3 * TILE < w1) issue_tile<G>(R, tb + 3 * TILE, S, tiles3[wave], lane);
+      process(tb, tiles0[wave]);
+      if (tb + TILE >= w1) break;
+      if (tb + 4 * TILE < w1) issue_tile<G>(R, tb + 4 * TILE, S, tiles0[wave], lane);
+      process(tb + TILE, tiles1[wave]);
+      if (tb + 2 * TILE >= w1) break;
+      if (tb + 5 * TILE < w1) issue_tile<G>(R, tb + 5 * TILE, S, tiles1[wave], lane);
+      process(tb + 2 * TILE, tiles2[wave]);
+      if (tb + 3 * TILE >= w1) break;
+      if (tb + 6 * TILE < w1) issue_tile<G>(R, tb + 6 * TILE, S, tiles2[wave], lane);
+      process(tb + 3 * TILE, tiles3[wave]);
+    }
+  } else {
+    for (int tb = w0; tb < w1; tb += 3 * TILE) {
+      if (tb + 2 * TILE < w1) issue_tile<G>(R, tb + 2 * TILE, S, tiles2[wave], lane);
+      process(tb, tiles0[wave]);
+      if (tb + TILE >= w1) break;
+      if (tb + 3 * TILE < w1) issue_tile<G>(R, tb + 3 * TILE, S, tiles0[wave], lane);
+      process(tb + TILE, tiles1[wave]);
+      if (tb + 2 * TILE >= w1) break;
+      if (tb + 4 * TILE < w1) issue_tile<G>(R, tb + 4 * TILE, S, tiles1[wave], lane);
+      process(tb + 2 * TILE, tiles2[wave]);
+    }
   }
 
-  // per-wave partial -> LDS
+  // per-wave partial -> LDS (in the wave's first tile buffer, whose last reads are complete)
+  // wave w's partial: o [NREP][FAST_D], then m [NREP] and l [NREP]
+  auto o_wave = [&](int w) -> float* {
+    if constexpr (O_IN_TILE) return (float*)&tiles0[w];
+    else return &o_sep[w * (NREP * FAST_D + 2 * NREP)];
+  };
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
   const bool own = colvalid && (q4 / CPG == colm);
+  float* ow = o_wave(wave);
   if (own) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        o_lds[wave][colh][32 * q4 + 8 * r + k] = acc[k][r] - 136.0f * corr[r];
+        ow[colh * FAST_D + 32 * q4 + 8 * r + k] = acc[k][r] - 136.0f * corr[r];
       }
     }
   }
   if (lane < NREP) {
-    ml_lds[wave][0][lane] = m_run;
-    ml_lds[wave][1][lane] = l_run;
+    ow[NREP * FAST_D + lane] = m_run;
+    ow[NREP * FAST_D + NREP + lane] = l_run;
   }
   __syncthreads();
 
   // merge the 4 waves
-  for (int idx = tid; idx < NREP * FAST_D; idx += 256) {
+  for (int idx = tid; idx < NREP * FAST_D; idx += THREADS) {
     const int h = idx / FAST_D;
     const int d = idx - h * FAST_D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, ml_lds[w][0][h]);
+    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, o_wave(w)[NREP * FAST_D + h]);
     float L = 0.0f;
     float a = 0.0f;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) {
-      const float mw = ml_lds[w][0][h];
+      const float mw = o_wave(w)[NREP * FAST_D + h];
       const float wt = (mw == -INFINITY) ? 0.0f : exp2f(mw - M);
-      L += wt * ml_lds[w][1][h];
-      a += wt * o_lds[w][h][d];
+      L += wt * o_wave(w)[NREP * FAST_D + NREP + h];
+      a += wt * o_wave(w)[h * FAST_D + d];
     }
     const int qh = kvh * NREP + h;
     if (p.nsplit == 1) {
@@ -498,8 +552,9 @@ bool fast_path_ok(const AttnParams& p) {
   return true;
 }
 
-// Waves of attn_fast_kernel resident on the current device at once: its register use (over 128
-// VGPRs) leaves 2 waves per SIMD, 4 SIMDs per CU.
+// Waves of attn_fast_kernel resident on the current device at once: CUs x the workgroups per CU
+// that the occupancy calculator gives for the <4, 4> instance (its register and LDS use stand for
+// the others') x 4 waves.
 static int64_t resident_fast_waves() {
   static int cached[64] = {0};
   int dev = 0;
@@ -510,7 +565,13 @@ static int64_t resident_fast_waves() {
         cus <= 0) {
       cus = 256;
     }
-    cached[dev] = cus * 4 * 2;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&attn_fast_kernel<4, 4>), THREADS, 0) != hipSuccess ||
+        per_cu <= 0) {
+      per_cu = 2;
+    }
+    cached[dev] = cus * per_cu * WAVES;
   }
   return cached[dev];
 }
@@ -532,7 +593,7 @@ SplitPlan plan_fast(int64_t B, int64_t Hkv, int64_t S) {
 template <int NREP, int G>
 static void launch_one(const AttnParams& p, hipStream_t st) {
   hipLaunchKernelGGL((attn_fast_kernel<NREP, G>), dim3((unsigned)(p.B * p.Hkv), (unsigned)p.nsplit),
-                     dim3(256), 0, st, p);
+                     dim3(THREADS), 0, st, p);
 }
 
 int launch_fast(const AttnParams& p, hipStream_t st) {
