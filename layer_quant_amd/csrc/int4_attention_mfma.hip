@@ -41,15 +41,11 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int FAST_D = 128;
-constexpr int SUB = 32;              // keys per MFMA sub-tile (the K depth of the P V product)
-constexpr int NSUB = 1;              // sub-tiles per iteration; one softmax max per iteration
-constexpr int TILE = SUB * NSUB;     // keys per wave iteration
+constexpr int TILE = 32;             // keys per wave iteration (the K depth of the P V product)
 constexpr int WAVES = 4;             // waves per workgroup, each on its own key range
 constexpr int THREADS = 64 * WAVES;
-constexpr int NBUF = 3;              // LDS tile buffers per wave (3 or 4; 4 measured no faster)
 constexpr float LAZY_LOG2 = 8.0f;    // running-max slack of the lazy softmax rescale
 constexpr uint32_t NIB2 = 0x000F000Fu;
 constexpr int BUF_DWORD3 = 0x00020000;  // raw 32-bit buffer, gfx9 family
@@ -214,15 +210,12 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   constexpr int NCOL = NREP * G;
   constexpr int CPG = 4 / G;  // 32-dim chunks per group
   static_assert(NCOL <= 16, "columns exceed the MFMA tile");
-  static_assert(NSUB == 1, "one 32-key sub-tile per tile");
-  static_assert(NBUF == 3 || NBUF == 4, "3 or 4 tile buffers");
-  // NBUF tile buffers per wave (separate LDS objects, one per ring position); a wave's partial
+  // 3 tile buffers per wave (separate LDS objects, one per ring position); a wave's partial
   // output and softmax state reuse its first buffer when they fit (NREP <= 8)
   constexpr bool O_IN_TILE = (NREP * FAST_D + 2 * NREP) * 4 <= (int)sizeof(TileLds);
   __shared__ TileLds tiles0[WAVES];
   __shared__ TileLds tiles1[WAVES];
   __shared__ TileLds tiles2[WAVES];
-  __shared__ TileLds tiles3[NBUF > 3 ? WAVES : 1];
   __shared__ float o_sep[O_IN_TILE ? 1 : WAVES * (NREP * FAST_D + 2 * NREP)];
 
   const int tid = threadIdx.x;
@@ -256,7 +249,6 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   // the first tiles' loads go out before the query set-up
   if (w0 < w1) issue_tile<G>(R, w0, S, tiles0[wave], lane);
   if (w0 + TILE < w1) issue_tile<G>(R, w0 + TILE, S, tiles1[wave], lane);
-  if (NBUF > 3 && w0 + 2 * TILE < w1) issue_tile<G>(R, w0 + 2 * TILE, S, tiles2[wave], lane);
 
   // Query operands. Lane (q, .) feeds MFMA c with dword c of its key unit q, i.e. dims
   // 32q + 8c .. 32q + 8c + 7 (slot order kPerm); the query is placed only in the columns whose
@@ -302,8 +294,7 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   // Before tile tb's reads: wait for its 6 loads, leaving the already issued loads of the
   // following tiles (6 each) in flight.
   auto wait_tile = [&](const int tb) {
-    if (NBUF > 3 && tb + 3 * TILE < w1) wait_loads<18>();
-    else if (tb + 2 * TILE < w1) wait_loads<12>();
+    if (tb + 2 * TILE < w1) wait_loads<12>();
     else if (tb + TILE < w1) wait_loads<6>();
     else wait_loads<0>();
   };
@@ -429,34 +420,18 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
     __builtin_amdgcn_wave_barrier();
   };
 
-  // NBUF-deep ring of LDS tiles: the loads of the next NBUF - 1 tiles are in flight while one
-  // is processed (the loop is unrolled by NBUF so that each buffer is a distinct LDS object and
-  // the compiler's wait before a buffer's reads counts only that buffer's loads)
-  if constexpr (NBUF > 3) {
-    for (int tb = w0; tb < w1; tb += 4 * TILE) {
-      if (tb + 3 * TILE < w1) issue_tile<G>(R, tb + 3 * TILE, S, tiles3[wave], lane);
-      process(tb, tiles0[wave]);
-      if (tb + TILE >= w1) break;
-      if (tb + 4 * TILE < w1) issue_tile<G>(R, tb + 4 * TILE, S, tiles0[wave], lane);
-      process(tb + TILE, tiles1[wave]);
-      if (tb + 2 * TILE >= w1) break;
-      if (tb + 5 * TILE < w1) issue_tile<G>(R, tb + 5 * TILE, S, tiles1[wave], lane);
-      process(tb + 2 * TILE, tiles2[wave]);
-      if (tb + 3 * TILE >= w1) break;
-      if (tb + 6 * TILE < w1) issue_tile<G>(R, tb + 6 * TILE, S, tiles2[wave], lane);
-      process(tb + 3 * TILE, tiles3[wave]);
-    }
-  } else {
-    for (int tb = w0; tb < w1; tb += 3 * TILE) {
-      if (tb + 2 * TILE < w1) issue_tile<G>(R, tb + 2 * TILE, S, tiles2[wave], lane);
-      process(tb, tiles0[wave]);
-      if (tb + TILE >= w1) break;
-      if (tb + 3 * TILE < w1) issue_tile<G>(R, tb + 3 * TILE, S, tiles0[wave], lane);
-      process(tb + TILE, tiles1[wave]);
-      if (tb + 2 * TILE >= w1) break;
-      if (tb + 4 * TILE < w1) issue_tile<G>(R, tb + 4 * TILE, S, tiles1[wave], lane);
-      process(tb + 2 * TILE, tiles2[wave]);
-    }
+  // 3-deep ring of LDS tiles: the loads of the next 2 tiles are in flight while one is processed
+  // (unrolled by 3 so that each ring position is its own LDS object; a 4th buffer, the whole
+  // 160 KB of LDS per CU at 2 workgroups, measured no faster)
+  for (int tb = w0; tb < w1; tb += 3 * TILE) {
+    if (tb + 2 * TILE < w1) issue_tile<G>(R, tb + 2 * TILE, S, tiles2[wave], lane);
+    process(tb, tiles0[wave]);
+    if (tb + TILE >= w1) break;
+    if (tb + 3 * TILE < w1) issue_tile<G>(R, tb + 3 * TILE, S, tiles0[wave], lane);
+    process(tb + TILE, tiles1[wave]);
+    if (tb + 2 * TILE >= w1) break;
+    if (tb + 4 * TILE < w1) issue_tile<G>(R, tb + 4 * TILE, S, tiles1[wave], lane);
+    process(tb + 2 * TILE, tiles2[wave]);
   }
 
   // per-wave partial -> LDS (in the wave's first tile buffer, whose last reads are complete)
