@@ -191,7 +191,9 @@ __device__ __forceinline__ void issue_tile(const Rsrc& R, int tb, int S, TileLds
   const i32x4_t rvs = make_desc(R.vsb + (int64_t)tb * G, rem * G * 4);
   // the tile's 32 G scale words of each kind: 16 bytes per lane on lanes 0..31 for G = 4, one
   // dword per lane on lanes below 32 G otherwise (16-byte units would straddle the end of the
-  // scales at a ragged S); the other lanes are inactive and write nothing
+  // scales at a ragged S); the other lanes are inactive and write nothing. issue_tile runs with
+  // all 64 lanes active, so lane 0 always issues these two loads and every tile counts 6 loads
+  // in the waits.
   if constexpr (G == 4) {
     if (lane < 32) {
       load_to_lds(rks, &B.ks[0], 16 * lane);

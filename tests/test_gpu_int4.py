@@ -162,6 +162,19 @@ def test_attention_bf16_output(gpu):
     assert_close_rel(out.float(), ref, rtol=8e-3, what="bf16 out")
 
 
+@pytest.mark.parametrize("s,g", [(999, 32), (1057, 64), (1150, 128)])
+def test_attention_long_wave_ranges_ragged_tail(gpu, s, g):
+    """B * Hkv = 512: each wave of the MFMA path walks 8-9 tiles of 32 keys through its 3-buffer
+    LDS ring, and the last wave's ragged tile lands on ring position 1, 0 and 2 for the three
+    contexts (one resident generation of 2048 waves, 4 waves per (batch, KV head))."""
+    b, hkv, nrep, d = 64, 8, 4, 128
+    cache = _packed_cache(b, hkv, s, d, g, 1200 + s, cap=s + 5)
+    q = _activations((b, hkv * nrep, 1, d), 1300 + s, torch.bfloat16)
+    ref = oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
+                               cache["v_scale"], s, nrep, g)
+    assert_close_rel(_run_attention(gpu, cache, q, s, nrep, g), ref, what="fast")
+
+
 @pytest.mark.parametrize("b,s", [(64, 16384), (8, 4096)])
 def test_attention_full_size_sampled_heads(gpu, b, s):
     """BASELINE sizes: random packed cache built on the GPU, oracle on sampled (b, kv head)."""
