@@ -2,7 +2,8 @@
 """Decode-step benchmark of the quantized Nemotron-H-8B paths on one MI355X.
 
 One step = the quantized work of one decode step of the hybrid stack at batch 64, context 16384:
-  4 attention layers:  INT4 pack of the new K and V token (2 calls) + q_len=1 decode attention
+  4 attention layers:  INT4 pack of the new K and V token (one lq_int4_pack_kv_pair call, as the
+                       module's _pack_kv_into_cache makes it) + q_len=1 decode attention
                        over the packed cache (32 query / 8 KV heads, head_dim 128, group 32)
   24 Mamba2 layers:    fused MX4 selective-state update (128 heads x 64 x 128, 8 groups,
                        stochastic writeback from the counter generator)
@@ -148,7 +149,7 @@ def build_workload(torch, args, dev):
     torch.cuda.synchronize()
     sizes = dict(
         attention=attention_bytes(B, hq, hkv, d, S, g),
-        pack=pack_bytes(B, hkv, 1, d, g),
+        pack=2 * pack_bytes(B, hkv, 1, d, g),  # K and V in one call
         mx_update=mx_update_bytes(B, nh, p_, n, ng, format_bits=args.state_bits,
                                   layout=args.state_layout),
     )
@@ -168,8 +169,9 @@ def run_step(torch, args, attn, mamba, ev=None):
             ev.around(name, fn)
 
     for L in attn:
-        call("pack", lambda: _abi.int4_pack_kv(L["k_new"], L["k_packed"], L["k_scale"], L["pos"], g))
-        call("pack", lambda: _abi.int4_pack_kv(L["v_new"], L["v_packed"], L["v_scale"], L["pos"], g))
+        call("pack", lambda: _abi.int4_pack_kv_pair(L["k_new"], L["v_new"], L["k_packed"],
+                                                    L["v_packed"], L["k_scale"], L["v_scale"],
+                                                    L["pos"], g))
         call("attention", lambda: _abi.int4_decode_attention(
             L["q"], L["k_packed"], L["v_packed"], L["k_scale"], L["v_scale"], None, L["out"], S,
             4, g))
@@ -296,8 +298,8 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
 
 
 def config1_gpu(torch, dev, reps: int = 20) -> float:
-    """BASELINE config 1 on the GPU through the C ABI: pack a 1024-token K/V cache (two
-    lq_int4_pack_kv calls) and attend once (lq_int4_decode_attention), batch 1, 32 q / 8 KV
+    """BASELINE config 1 on the GPU through the C ABI: pack a 1024-token K/V cache (one
+    lq_int4_pack_kv_pair call) and attend once (lq_int4_decode_attention), batch 1, 32 q / 8 KV
     heads, group 32; median us per repetition (HIP events)."""
     from layer_quant_amd import _abi
 
@@ -314,8 +316,7 @@ def config1_gpu(torch, dev, reps: int = 20) -> float:
     out = torch.empty(1, hq, d, device=dev, dtype=torch.bfloat16)
 
     def once():
-        _abi.int4_pack_kv(k, kp, ks, pos, g)
-        _abi.int4_pack_kv(v, vp, vs, pos, g)
+        _abi.int4_pack_kv_pair(k, v, kp, vp, ks, vs, pos, g)
         _abi.int4_decode_attention(q, kp, vp, ks, vs, None, out, S, hq // hkv, g)
 
     once()
@@ -483,7 +484,7 @@ def main():
         kernels[name] = {"us": round(us, 2), "algorithmic_bytes": nbytes,
                          "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
                          "calls_per_step": {"attention": args.attn_layers,
-                                            "pack": 2 * args.attn_layers,
+                                            "pack": args.attn_layers,
                                             "mx_update": args.mamba_layers}[name]}
         log(f"{name}: {us:.1f} us/call, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%})")
     dominant = max(kernels, key=lambda k: kernels[k]["us"] * kernels[k]["calls_per_step"])
@@ -494,7 +495,7 @@ def main():
         "kernel": {"attention": "lq_int4_decode_attention (attn_fast_kernel, + attn_merge_kernel "
                                 "when split)",
                    "mx_update": f"lq_mx_state_update (mx_update_rows_kernel MX{args.state_bits})",
-                   "pack": "lq_int4_pack_kv"}[dominant],
+                   "pack": "lq_int4_pack_kv_pair"}[dominant],
         "bound": "hbm",
         "achieved": dk["GB_s"],
         "peak": PEAK_HBM_GBS,

@@ -97,6 +97,17 @@ int lq_int4_pack_kv(const lq_tensor* x, const lq_tensor* packed, const lq_tensor
                     const lq_tensor* positions, int group_size, void* stream);
 
 /*
+ * lq_int4_pack_kv for a layer's K and V in one launch (the same arguments and checks, applied to
+ * (k, k_packed, k_scale) and (v, v_packed, v_scale) with shared positions).
+ * No counterpart in the reference: it replaces the pair of _pack_int4_kv_kernel launches that
+ * _pack_kv_into_cache makes (hybrid_quant/int4_8b_attention.py:487-514) with one.
+ */
+int lq_int4_pack_kv_pair(const lq_tensor* k, const lq_tensor* v, const lq_tensor* k_packed,
+                         const lq_tensor* v_packed, const lq_tensor* k_scale,
+                         const lq_tensor* v_scale, const lq_tensor* positions, int group_size,
+                         void* stream);
+
+/*
  * Workspace bytes that lq_int4_decode_attention needs for this shape (0 if none).
  * No counterpart in the reference (its decode kernel has no split-K); it sizes the split-K
  * partials of the kernel below.

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "lq_abi_version",
     "lq_last_error",
     "lq_int4_pack_kv",
+    "lq_int4_pack_kv_pair",
     "lq_int4_decode_attention_workspace",
     "lq_int4_decode_attention",
     "lq_int4_prefill_attention",
@@ -82,6 +83,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.lq_last_error.argtypes = []
     lib.lq_int4_pack_kv.restype = ctypes.c_int
     lib.lq_int4_pack_kv.argtypes = [_P, _P, _P, _P, ctypes.c_int, ctypes.c_void_p]
+    lib.lq_int4_pack_kv_pair.restype = ctypes.c_int
+    lib.lq_int4_pack_kv_pair.argtypes = [_P] * 7 + [ctypes.c_int, ctypes.c_void_p]
     lib.lq_int4_decode_attention_workspace.restype = ctypes.c_size_t
     lib.lq_int4_decode_attention_workspace.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int]
     lib.lq_int4_decode_attention.restype = ctypes.c_int
@@ -182,6 +185,17 @@ def int4_pack_kv(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor,
     rc = lib().lq_int4_pack_kv(desc(x), desc(packed), desc(scale), desc(positions),
                                int(group_size), _stream(dev))
     check(rc, "lq_int4_pack_kv")
+
+
+def int4_pack_kv_pair(k: torch.Tensor, v: torch.Tensor, k_packed: torch.Tensor,
+                      v_packed: torch.Tensor, k_scale: torch.Tensor, v_scale: torch.Tensor,
+                      positions: torch.Tensor, group_size: int) -> None:
+    """int4_pack_kv of a layer's K and V in one launch."""
+    dev = _require_gpu(k, v, k_packed, v_packed, k_scale, v_scale, positions)
+    rc = lib().lq_int4_pack_kv_pair(desc(k), desc(v), desc(k_packed), desc(v_packed),
+                                    desc(k_scale), desc(v_scale), desc(positions),
+                                    int(group_size), _stream(dev))
+    check(rc, "lq_int4_pack_kv_pair")
 
 
 class _Workspace:

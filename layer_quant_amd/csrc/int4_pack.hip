@@ -5,7 +5,10 @@
 // (IEEE division, round half to even) -> clamp [-8, 7] -> two's-complement nibbles, even d in the
 // low nibble. int4_pack_lanes_kernel gives one lane to each output byte (dims 2j, 2j+1), so a
 // group is g/2 adjacent lanes and its absmax a shuffle reduction; int4_pack_kernel (one thread
-// per group) covers group sizes whose g/2 is not a power of two up to 64.
+// per group) covers group sizes whose g/2 is not a power of two up to 64. Both kernels take up to
+// two tensors (blockIdx.y picks one): lq_int4_pack_kv_pair packs a layer's K and V in one launch.
+#include <algorithm>
+
 #include "lq_common.h"
 
 namespace lq {
@@ -22,12 +25,19 @@ struct PackParams {
   int64_t cap;
 };
 
+// The tensors of one launch: pp[blockIdx.y] (one entry used by lq_int4_pack_kv).
+struct PackPair {
+  PackParams pp[2];
+};
+
 // One lane per packed byte; GH = g/2 lanes per group (a power of two <= 64, so groups never
 // straddle a wave). Lane offsets are 32-bit (the host checks the element count).
 template <int GH>
-__global__ __launch_bounds__(256) void int4_pack_lanes_kernel(PackParams p) {
+__global__ __launch_bounds__(256) void int4_pack_lanes_kernel(PackPair pair) {
+  const PackParams& p = pair.pp[blockIdx.y];
   const int half = p.D >> 1;
   const int total = p.B * p.H * p.T * half;
+  if (total == 0) return;  // an empty tensor of a pair
   const int gid = blockIdx.x * 256 + threadIdx.x;
   const bool in = gid < total;
   const int g2 = in ? gid : total - 1;  // whole trailing groups only; they store nothing
@@ -55,7 +65,8 @@ __global__ __launch_bounds__(256) void int4_pack_lanes_kernel(PackParams p) {
   }
 }
 
-__global__ __launch_bounds__(256) void int4_pack_kernel(PackParams p) {
+__global__ __launch_bounds__(256) void int4_pack_kernel(PackPair pair) {
+  const PackParams& p = pair.pp[blockIdx.y];
   const int groups = p.D / p.g;
   const int64_t total = (int64_t)p.B * p.H * p.T * groups;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -94,9 +105,11 @@ __global__ __launch_bounds__(256) void int4_pack_kernel(PackParams p) {
 
 using namespace lq;
 
-extern "C" int lq_int4_pack_kv(const lq_tensor* x, const lq_tensor* packed,
-                               const lq_tensor* scale, const lq_tensor* positions,
-                               int group_size, void* stream) {
+namespace {
+
+// Validate one (x, packed, scale) triple against positions and fill its launch parameters.
+int make_pack_params(const lq_tensor* x, const lq_tensor* packed, const lq_tensor* scale,
+                     const lq_tensor* positions, int group_size, PackParams& p) {
   int rc;
   if ((rc = check_tensor(x, "x", 4, true)) != LQ_OK) return rc;
   if ((rc = check_tensor(packed, "packed", 4, false, LQ_U8)) != LQ_OK) return rc;
@@ -124,9 +137,7 @@ extern "C" int lq_int4_pack_kv(const lq_tensor* x, const lq_tensor* packed,
     return fail(LQ_ERR_INVALID_ARG, "positions has %lld entries for q_len=%lld",
                 (long long)positions->shape[0], (long long)T);
   }
-  if (B == 0 || H == 0 || T == 0 || D == 0) return LQ_OK;
-
-  PackParams p{};
+  p = PackParams{};
   p.x = make_view(x);
   p.packed = (uint8_t*)packed->data;
   p.scale = (float*)scale->data;
@@ -142,25 +153,64 @@ extern "C" int lq_int4_pack_kv(const lq_tensor* x, const lq_tensor* packed,
   p.D = (int)D;
   p.g = group_size;
   p.cap = cap;
-  hipStream_t s = (hipStream_t)stream;
-  const int gh = group_size / 2;
-  const int64_t bytes = B * H * T * (D / 2);
-  if (gh <= 64 && (gh & (gh - 1)) == 0 && bytes < ((int64_t)1 << 31) - 256) {
-    const dim3 grid((unsigned)((bytes + 255) / 256));
-    switch (gh) {
-      case 1: hipLaunchKernelGGL(int4_pack_lanes_kernel<1>, grid, dim3(256), 0, s, p); break;
-      case 2: hipLaunchKernelGGL(int4_pack_lanes_kernel<2>, grid, dim3(256), 0, s, p); break;
-      case 4: hipLaunchKernelGGL(int4_pack_lanes_kernel<4>, grid, dim3(256), 0, s, p); break;
-      case 8: hipLaunchKernelGGL(int4_pack_lanes_kernel<8>, grid, dim3(256), 0, s, p); break;
-      case 16: hipLaunchKernelGGL(int4_pack_lanes_kernel<16>, grid, dim3(256), 0, s, p); break;
-      case 32: hipLaunchKernelGGL(int4_pack_lanes_kernel<32>, grid, dim3(256), 0, s, p); break;
-      default: hipLaunchKernelGGL(int4_pack_lanes_kernel<64>, grid, dim3(256), 0, s, p); break;
-    }
-    return check_launch("lq_int4_pack_kv");
+  return LQ_OK;
+}
+
+int64_t pack_bytes(const PackParams& p) { return (int64_t)p.B * p.H * p.T * (p.D / 2); }
+
+// One launch over pair.pp[0 .. n-1] (n = 1 or 2), sized for the larger tensor.
+int launch_pack(const PackPair& pair, int n, int group_size, hipStream_t s, const char* what) {
+  int64_t bytes = 0, groups = 0;
+  for (int i = 0; i < n; ++i) {
+    bytes = std::max(bytes, pack_bytes(pair.pp[i]));
+    groups = std::max(groups, pack_bytes(pair.pp[i]) * 2 / group_size);
   }
-  const int64_t total = B * H * T * (D / group_size);
+  if (bytes == 0) return LQ_OK;
+  const int gh = group_size / 2;
+  if (gh <= 64 && (gh & (gh - 1)) == 0 && bytes < ((int64_t)1 << 31) - 256) {
+    const dim3 grid((unsigned)((bytes + 255) / 256), (unsigned)n);
+    switch (gh) {
+      case 1: hipLaunchKernelGGL(int4_pack_lanes_kernel<1>, grid, dim3(256), 0, s, pair); break;
+      case 2: hipLaunchKernelGGL(int4_pack_lanes_kernel<2>, grid, dim3(256), 0, s, pair); break;
+      case 4: hipLaunchKernelGGL(int4_pack_lanes_kernel<4>, grid, dim3(256), 0, s, pair); break;
+      case 8: hipLaunchKernelGGL(int4_pack_lanes_kernel<8>, grid, dim3(256), 0, s, pair); break;
+      case 16: hipLaunchKernelGGL(int4_pack_lanes_kernel<16>, grid, dim3(256), 0, s, pair); break;
+      case 32: hipLaunchKernelGGL(int4_pack_lanes_kernel<32>, grid, dim3(256), 0, s, pair); break;
+      default: hipLaunchKernelGGL(int4_pack_lanes_kernel<64>, grid, dim3(256), 0, s, pair); break;
+    }
+    return check_launch(what);
+  }
   const int threads = 256;
-  const int64_t blocks = (total + threads - 1) / threads;
-  hipLaunchKernelGGL(int4_pack_kernel, dim3((unsigned)blocks), dim3(threads), 0, s, p);
-  return check_launch("lq_int4_pack_kv");
+  const int64_t blocks = (groups + threads - 1) / threads;
+  hipLaunchKernelGGL(int4_pack_kernel, dim3((unsigned)blocks, (unsigned)n), dim3(threads), 0, s,
+                     pair);
+  return check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int lq_int4_pack_kv(const lq_tensor* x, const lq_tensor* packed,
+                               const lq_tensor* scale, const lq_tensor* positions,
+                               int group_size, void* stream) {
+  PackPair pair{};
+  int rc;
+  if ((rc = make_pack_params(x, packed, scale, positions, group_size, pair.pp[0])) != LQ_OK) {
+    return rc;
+  }
+  return launch_pack(pair, 1, group_size, (hipStream_t)stream, "lq_int4_pack_kv");
+}
+
+extern "C" int lq_int4_pack_kv_pair(const lq_tensor* k, const lq_tensor* v,
+                                    const lq_tensor* k_packed, const lq_tensor* v_packed,
+                                    const lq_tensor* k_scale, const lq_tensor* v_scale,
+                                    const lq_tensor* positions, int group_size, void* stream) {
+  PackPair pair{};
+  int rc;
+  if ((rc = make_pack_params(k, k_packed, k_scale, positions, group_size, pair.pp[0])) != LQ_OK) {
+    return rc;
+  }
+  if ((rc = make_pack_params(v, v_packed, v_scale, positions, group_size, pair.pp[1])) != LQ_OK) {
+    return rc;
+  }
+  return launch_pack(pair, 2, group_size, (hipStream_t)stream, "lq_int4_pack_kv_pair");
 }

@@ -118,9 +118,10 @@ def _ensure_layer_cache(past_key_value, layer_idx: int, batch: int, kv_heads: in
 def _pack_kv_into_cache(cache: Int4KVLayerCache, key_states: torch.Tensor,
                         value_states: torch.Tensor, positions: torch.Tensor,
                         group_size: int) -> None:
-    """INT4-pack K and V [B, Hkv, q_len, D] into rows `positions` (ia.py:477-515)."""
-    _abi.int4_pack_kv(key_states, cache.k_packed, cache.k_scale, positions, group_size)
-    _abi.int4_pack_kv(value_states, cache.v_packed, cache.v_scale, positions, group_size)
+    """INT4-pack K and V [B, Hkv, q_len, D] into rows `positions` (ia.py:477-515); one launch
+    for both (the reference launches _pack_int4_kv_kernel once for K and once for V)."""
+    _abi.int4_pack_kv_pair(key_states, value_states, cache.k_packed, cache.v_packed,
+                           cache.k_scale, cache.v_scale, positions, group_size)
     cache.length = max(cache.length, int(positions.max().item()) + 1)
 
 

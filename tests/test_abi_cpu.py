@@ -66,6 +66,27 @@ def test_pack_rejects_bad_arguments():
     assert "q_len" in _abi.last_error()
 
 
+def test_pack_pair_rejects_bad_arguments():
+    """Each of the two triples goes through the single-tensor checks before anything launches."""
+    lib = _abi.lib()
+    x = _fake((2, 8, 1, 128), torch.bfloat16)
+    packed = _fake((2, 8, 16, 64), torch.uint8)
+    scale = _fake((2, 8, 16, 4), torch.float32)
+    pos = _fake((1,), torch.int64)
+    f = lib.lq_int4_pack_kv_pair
+    assert f(None, x, packed, packed, scale, scale, pos, 32, None) == _abi.LQ_ERR_INVALID_ARG
+    assert f(x, None, packed, packed, scale, scale, pos, 32, None) == _abi.LQ_ERR_INVALID_ARG
+    assert f(x, x, packed, packed, scale, scale, pos, 31, None) == _abi.LQ_ERR_INVALID_ARG
+    assert "even" in _abi.last_error()
+    bad_scale = _fake((2, 8, 16, 2), torch.float32)
+    assert f(x, x, packed, packed, scale, bad_scale, pos, 32, None) == _abi.LQ_ERR_INVALID_ARG
+    assert "scale must be" in _abi.last_error()
+    bad_packed = _fake((2, 8, 16, 32), torch.uint8)
+    assert f(x, x, packed, bad_packed, scale, scale, pos, 32, None) == _abi.LQ_ERR_INVALID_ARG
+    two_pos = _fake((2,), torch.int64)
+    assert f(x, x, packed, packed, scale, scale, two_pos, 32, None) == _abi.LQ_ERR_INVALID_ARG
+
+
 def test_attention_rejects_bad_arguments():
     lib = _abi.lib()
     kp = _fake((2, 8, 64, 64), torch.uint8)

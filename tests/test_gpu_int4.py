@@ -54,6 +54,40 @@ def test_pack_bit_exact_other_groups(gpu, g, d):
     assert torch.equal(scale.cpu(), ref_s)
 
 
+@pytest.mark.parametrize("g,t,dtype", [(32, 1, torch.bfloat16), (64, 5, torch.float32),
+                                       (128, 1, torch.float16), (48, 3, torch.bfloat16)])
+def test_pack_pair_equals_two_single_packs(gpu, g, t, dtype):
+    """lq_int4_pack_kv_pair writes exactly what two lq_int4_pack_kv calls write, including a V
+    given as a transposed view (different strides from K); g = 48 takes the per-group kernel."""
+    b, hkv, d, cap = 3, 8, 96 if g == 48 else 128, 12
+    k = _activations((b, hkv, t, d), 40 + g, dtype).to(gpu)
+    v = _activations((b, t, hkv, d), 50 + g, dtype).to(gpu).transpose(1, 2)
+    pos = torch.tensor([2, 7, 0, 11, 5][:t], device=gpu)
+    outs = []
+    for pair in (True, False):
+        kp = torch.full((b, hkv, cap, d // 2), 0x5A, dtype=torch.uint8, device=gpu)
+        vp = torch.full_like(kp, 0xA5)
+        ks = torch.full((b, hkv, cap, d // g), -1.0, device=gpu)
+        vs = torch.full_like(ks, -2.0)
+        if pair:
+            _abi.int4_pack_kv_pair(k, v, kp, vp, ks, vs, pos, g)
+        else:
+            _abi.int4_pack_kv(k, kp, ks, pos, g)
+            _abi.int4_pack_kv(v, vp, vs, pos, g)
+        torch.cuda.synchronize()
+        outs.append((kp.cpu(), vp.cpu(), ks.cpu(), vs.cpu()))
+    for a_, b_ in zip(*outs):
+        assert torch.equal(a_, b_)
+    ref = oik.allocate_cache(b, hkv, cap, d, g)
+    oik.pack_into(ref["k_packed"], ref["k_scale"], k.cpu(), pos.cpu(), g)
+    oik.pack_into(ref["v_packed"], ref["v_scale"], v.cpu(), pos.cpu(), g)
+    rows = pos.cpu()
+    assert torch.equal(outs[0][0][:, :, rows], ref["k_packed"][:, :, rows])
+    assert torch.equal(outs[0][1][:, :, rows], ref["v_packed"][:, :, rows])
+    assert torch.equal(outs[0][2][:, :, rows], ref["k_scale"][:, :, rows])
+    assert torch.equal(outs[0][3][:, :, rows], ref["v_scale"][:, :, rows])
+
+
 def test_pack_edge_values(gpu):
     d, g = 128, 32
     x = torch.zeros(1, 1, 4, d)
