@@ -1,0 +1,99 @@
+"""A decode step captured in a HIP graph (through torch.cuda.CUDAGraph): fused K+V pack, decode
+attention with split-K partials in the per-stream workspace, and an MX4 state update with the
+counter generator. Three replays, with eager GPU work and synchronizations between them, each
+match the same calls run eagerly, bit for bit. None of these entry points records a memset."""
+import pytest
+import torch
+
+from layer_quant_amd import _abi
+
+pytestmark = pytest.mark.gpu
+
+
+def _make_state(gpu, seed):
+    gen = torch.Generator(device=gpu).manual_seed(seed)
+    b, hkv, nrep, s, d, g = 2, 8, 4, 1000, 128, 32   # B * Hkv = 16: several key splits
+    cap = s + 8
+    t = dict(
+        kp=torch.randint(0, 256, (b, hkv, cap, d // 2), dtype=torch.uint8, device=gpu, generator=gen),
+        vp=torch.randint(0, 256, (b, hkv, cap, d // 2), dtype=torch.uint8, device=gpu, generator=gen),
+        ks=torch.rand(b, hkv, cap, d // g, device=gpu, generator=gen) + 0.01,
+        vs=torch.rand(b, hkv, cap, d // g, device=gpu, generator=gen) + 0.01,
+        k_new=torch.randn(b, hkv, 1, d, device=gpu, generator=gen).to(torch.bfloat16),
+        v_new=torch.randn(b, hkv, 1, d, device=gpu, generator=gen).to(torch.bfloat16),
+        pos=torch.tensor([s - 1], device=gpu),
+        q=torch.randn(b, hkv * nrep, 1, d, device=gpu, generator=gen).to(torch.bfloat16),
+        att=torch.empty(b, hkv * nrep, d, device=gpu),
+    )
+    bsz, nh, p_, n, ng = 2, 16, 64, 128, 2
+    h0 = torch.randn(bsz, nh, p_, n, device=gpu, generator=gen) * 0.5
+    st = (torch.empty(bsz, nh, p_, n, dtype=torch.int8, device=gpu),
+          torch.empty(bsz, nh, p_, n // 16, dtype=torch.uint8, device=gpu),
+          torch.empty(bsz, nh, p_, n // 2, dtype=torch.uint8, device=gpu))
+    _abi.mx_encode(h0, *st, 4, _abi.ROUND_NEAREST_EVEN)
+    t.update(
+        st=st,
+        x=torch.randn(bsz, nh, p_, device=gpu, generator=gen).to(torch.bfloat16),
+        dt=torch.randn(bsz, nh, device=gpu, generator=gen).to(torch.bfloat16)[:, :, None].expand(bsz, nh, p_),
+        A=(-torch.exp(torch.rand(nh, device=gpu, generator=gen) * 2))[:, None, None].expand(nh, p_, n),
+        B=torch.randn(bsz, ng, n, device=gpu, generator=gen).to(torch.bfloat16),
+        C=torch.randn(bsz, ng, n, device=gpu, generator=gen).to(torch.bfloat16),
+        D=torch.randn(nh, device=gpu, generator=gen)[:, None].expand(nh, p_),
+        dt_bias=(torch.randn(nh, device=gpu, generator=gen) * 0.1)[:, None].expand(nh, p_),
+        y=torch.empty(bsz, nh, p_, device=gpu, dtype=torch.bfloat16),
+    )
+    t["dims"] = (s, nrep, g)
+    return t
+
+
+def _step(t):
+    s, nrep, g = t["dims"]
+    _abi.int4_pack_kv_pair(t["k_new"], t["v_new"], t["kp"], t["vp"], t["ks"], t["vs"], t["pos"], g)
+    _abi.int4_decode_attention(t["q"], t["kp"], t["vp"], t["ks"], t["vs"], None, t["att"], s, nrep, g)
+    _abi.mx_state_update(*t["st"], t["x"], t["dt"], t["dt_bias"], t["A"], t["B"], t["C"], t["D"],
+                         None, t["y"], 4, True, _abi.ROUND_SR_COUNTER, seed=1234, rng_offset=4096)
+
+
+def _snapshot(t):
+    return [x.clone() for x in (t["kp"], t["vp"], t["ks"], t["vs"], t["att"], t["y"], *t["st"])]
+
+
+def _restore(t, snap):
+    for dst, src in zip((t["kp"], t["vp"], t["ks"], t["vs"], t["att"], t["y"], *t["st"]), snap):
+        dst.copy_(src)
+
+
+def test_decode_step_graph_replays_match_eager(gpu):
+    t = _make_state(gpu, 2024)
+    start = _snapshot(t)
+    eager = []
+    for _ in range(3):  # the state update feeds the next step's state
+        _step(t)
+        torch.cuda.synchronize()
+        eager.append(_snapshot(t))
+
+    # warm up on a side stream (torch's recommended order), then capture from the start state
+    _restore(t, start)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _step(t)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _step(t)
+    torch.cuda.synchronize()
+
+    _restore(t, start)
+    torch.cuda.synchronize()
+    junk = torch.randn(1 << 20, device=gpu)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        got = _snapshot(t)
+        for a, b in zip(got, eager[i]):
+            assert torch.equal(a, b), f"replay {i}"
+        junk = junk * 1.0001 + 1.0  # eager work between replays
+        torch.cuda.synchronize()
+    assert torch.isfinite(t["att"]).all()
