@@ -232,6 +232,37 @@ def test_attention_repeats_bit_identical(gpu, b, hkv, nrep, s, g):
     assert torch.isfinite(ref).all()
 
 
+def test_attention_concurrent_streams(gpu):
+    """Split-K calls in flight on two streams at once use separate workspaces (one per stream):
+    each stream's results equal the same calls made one at a time on the default stream."""
+    b, hkv, nrep, d, g = 2, 8, 4, 128, 32
+    cases = []
+    for i, s in enumerate((3000, 1777)):
+        cache = _packed_cache(b, hkv, s, d, g, 1500 + i)
+        dev = {k: v.to(gpu) for k, v in cache.items() if torch.is_tensor(v)}
+        q = _activations((b, hkv * nrep, 1, d), 1600 + i).to(gpu)
+        cases.append((dev, q, s))
+    ref = []
+    for dev, q, s in cases:
+        out = torch.empty(b, hkv * nrep, d, device=gpu)
+        _abi.int4_decode_attention(q, dev["k_packed"], dev["v_packed"], dev["k_scale"],
+                                   dev["v_scale"], None, out, s, nrep, g)
+        ref.append(out)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[torch.empty_like(r) for _ in range(8)] for r in ref]
+    for it in range(8):
+        for (dev, q, s), st, o in zip(cases, streams, outs):
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                _abi.int4_decode_attention(q, dev["k_packed"], dev["v_packed"], dev["k_scale"],
+                                           dev["v_scale"], None, o[it], s, nrep, g)
+    torch.cuda.synchronize()
+    for r, o in zip(ref, outs):
+        for x in o:
+            assert torch.equal(x, r)
+
+
 @pytest.mark.parametrize("b,s", [(64, 16384), (8, 4096)])
 def test_attention_full_size_sampled_heads(gpu, b, s):
     """BASELINE sizes: random packed cache built on the GPU, oracle on sampled (b, kv head)."""
