@@ -183,6 +183,9 @@ __global__ __launch_bounds__(MERGE_THREADS) void attn_merge_kernel(AttnParams p)
   for (int d = d0; d < D; d += dw) {
     float acc = 0.0f;
     if (g < groups) {
+      // unrolled so that eight splits' loads are in flight before the first is used (one load
+      // at a time left the merge latency-bound: 10.4 us at 64 splits, batch 1, ctx 16384)
+#pragma unroll 8
       for (int s = g; s < ns; s += groups) {
         const float ms = p.ws_m[base + s];
         const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
