@@ -286,3 +286,40 @@ def test_full_size_b64_dt_zero_bit_exact(gpu, fb):
     h = omx.mx_decode(q0, e0, m0)
     ref = omx.mx_encode(h, fb, omx.ROUND_SR_COUNTER, seed=1234, rng_offset=off)
     _assert_mx_equal(st, ref)
+
+
+@pytest.mark.parametrize("fb", [4, 8])
+def test_full_size_b64_uniform_update_sampled_groups(gpu, fb):
+    """Headline size (B=64, 128 heads x 64 x 128, 8 groups, the model's layout) with a real update
+    (softplus dt, decay, B x, y with D) and the supplied-uniform writeback: three (batch, group)
+    slices of 16 heads against the oracle run on the same slices of the inputs."""
+    bsz, nh, p_, n, ng = 64, 128, 64, 128, 8
+    shape = (bsz, nh, p_, n)
+    gen = torch.Generator(device=gpu).manual_seed(640 + fb)
+    h0 = torch.randn(shape, device=gpu, generator=gen) * 0.5
+    st = _mx_tensors(shape, gpu)
+    _abi.mx_encode(h0, *st, fb, 0)
+    del h0
+    st0 = [a.clone() for a in st]
+    x = torch.randn(bsz, nh, p_, device=gpu, generator=gen).to(torch.bfloat16)
+    dt = torch.randn(bsz, nh, 1, device=gpu, generator=gen).to(torch.bfloat16).expand(bsz, nh, p_)
+    A = (-torch.exp(torch.rand(nh, device=gpu, generator=gen) * 2))[:, None, None].expand(nh, p_, n)
+    B = torch.randn(bsz, ng, n, device=gpu, generator=gen).to(torch.bfloat16)
+    C = torch.randn(bsz, ng, n, device=gpu, generator=gen).to(torch.bfloat16)
+    D = torch.randn(nh, device=gpu, generator=gen)[:, None].expand(nh, p_)
+    dt_bias = (torch.randn(nh, device=gpu, generator=gen) * 0.1)[:, None].expand(nh, p_)
+    uni = torch.rand(shape, device=gpu, generator=gen)
+    out = torch.empty(bsz, nh, p_, device=gpu)
+    _abi.mx_state_update(*st, x, dt, dt_bias, A, B, C, D, None, out, fb, True,
+                         _abi.ROUND_SR_UNIFORM, uniform=uni)
+    torch.cuda.synchronize()
+    hpg = nh // ng
+    for b, g in [(0, 0), (63, 7), (31, 3)]:
+        bs, hs = slice(b, b + 1), slice(g * hpg, (g + 1) * hpg)
+        q, e, m = (a[bs, hs].cpu().numpy() for a in st0)
+        rq, re_, rm, ry, _ = omx.mx_update(
+            q, e, m, x[bs, hs].cpu(), dt[bs, hs].cpu(), A[hs].cpu(), B[bs, g:g + 1].cpu(),
+            C[bs, g:g + 1].cpu(), D=D[hs].cpu(), dt_bias=dt_bias[hs].cpu(), dt_softplus=True,
+            format_bits=fb, round_mode=2, uniform=uni[bs, hs].cpu())
+        assert_close_rel(out[bs, hs].cpu(), ry, what=f"y b{b} g{g}")
+        _assert_state_close([a[bs, hs].cpu().numpy() for a in st], (rq, re_, rm))
