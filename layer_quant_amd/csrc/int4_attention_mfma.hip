@@ -106,6 +106,7 @@ struct alignas(16) TileLds {
   u32x4_t v[2][64];
   float ks[TILE * 4];  // [key][group] (G <= 4)
   float vs[TILE * 4];
+  float mk[TILE];      // additive mask of the tile's keys (masked calls only)
 };
 
 typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
@@ -172,11 +173,18 @@ struct Rsrc {
   const float* ksb;
   const float* vsb;
   int kvo;  // this lane's source offset for the swizzled K slot
+  const float* mb;     // mask row of this batch (masked calls)
+  int msk_bytes;       // its key stride in bytes
+  int64_t mask_len;    // keys the mask covers
 };
 
-// Issue the 6 loads of the tile at key tb into B (2 for K, 2 for V, one each for the K and V
-// scales on lanes below 8 G).
-template <int G>
+// Loads issued per tile (and counted by the waits): K 2, V 2, scales 2, and the mask row.
+template <bool MASK>
+constexpr int tile_loads() { return MASK ? 7 : 6; }
+
+// Issue the loads of the tile at key tb into B (2 for K, 2 for V, one each for the K and V
+// scales on lanes below 8 G, and with MASK one for the tile's 32 mask values).
+template <int G, bool MASK>
 __device__ __forceinline__ void issue_tile(const Rsrc& R, int tb, int S, TileLds& B, int lane) {
   tb = __builtin_amdgcn_readfirstlane(tb);  // uniform by construction; descriptors in SGPRs
   const int rem = S - tb;  // > 0
@@ -205,10 +213,18 @@ __device__ __forceinline__ void issue_tile(const Rsrc& R, int tb, int S, TileLds
       load_to_lds_b32(rvs, &B.vs[0], 4 * lane);
     }
   }
+  if constexpr (MASK) {
+    // keys at or past the mask's length read 0 here and are set to -inf by the score code
+    const int64_t mrem = R.mask_len - tb;
+    const i32x4_t rm = make_desc(R.mb + (int64_t)tb * (R.msk_bytes >> 2),
+                                 mrem > 0 ? (int)mrem * R.msk_bytes : 0);
+    if (lane < TILE) load_to_lds_b32(rm, &B.mk[0], lane * R.msk_bytes);
+  }
 }
 
-template <int NREP, int G>
+template <int NREP, int G, bool MASK>
 __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
+  constexpr int LPT = tile_loads<MASK>();
   constexpr int NCOL = NREP * G;
   constexpr int CPG = 4 / G;  // 32-dim chunks per group
   static_assert(NCOL <= 16, "columns exceed the MFMA tile");
@@ -247,10 +263,13 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   R.vsb = p.vs + b * p.vss[0] + kvh * p.vss[1];
   // K slot l of a half holds row l >> 2, unit (l & 3) ^ ((l >> 4) & 3)
   R.kvo = (lane >> 2) * 64 + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
+  R.mb = MASK ? p.mask + b * p.mask_sb : nullptr;
+  R.msk_bytes = (int)(p.mask_sk * 4);
+  R.mask_len = p.mask_len;
 
   // the first tiles' loads go out before the query set-up
-  if (w0 < w1) issue_tile<G>(R, w0, S, tiles0[wave], lane);
-  if (w0 + TILE < w1) issue_tile<G>(R, w0 + TILE, S, tiles1[wave], lane);
+  if (w0 < w1) issue_tile<G, MASK>(R, w0, S, tiles0[wave], lane);
+  if (w0 + TILE < w1) issue_tile<G, MASK>(R, w0 + TILE, S, tiles1[wave], lane);
 
   // Query operands. Lane (q, .) feeds MFMA c with dword c of its key unit q, i.e. dims
   // 32q + 8c .. 32q + 8c + 7 (slot order kPerm); the query is placed only in the columns whose
@@ -293,11 +312,11 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   f32x4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
   const u32x4_t ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
 
-  // Before tile tb's reads: wait for its 6 loads, leaving the already issued loads of the
-  // following tiles (6 each) in flight.
+  // Before tile tb's reads: wait for its loads, leaving the already issued loads of the
+  // following tiles (LPT each) in flight.
   auto wait_tile = [&](const int tb) {
-    if (tb + 2 * TILE < w1) wait_loads<12>();
-    else if (tb + TILE < w1) wait_loads<6>();
+    if (tb + 2 * TILE < w1) wait_loads<2 * LPT>();
+    else if (tb + TILE < w1) wait_loads<LPT>();
     else wait_loads<0>();
   };
 
@@ -354,12 +373,20 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
       s[e] = column_sum<NREP>(sacc[e >> 2][e & 3], B.ks[key * G + colm]);
       vsc[e] = B.vs[key * G + colm];
     }
-    if (p.mask != nullptr) {
+    if constexpr (MASK) {  // additive mask in raw score units; keys past its length are -inf
+      float mv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int tok = tb + 16 * (e >> 2) + 4 * (e & 3) + q4;
-        s[e] += (tok < p.mask_len) ? p.mask[b * p.mask_sb + (int64_t)tok * p.mask_sk] * inv_csm
-                                   : -INFINITY;
+      for (int e = 0; e < 8; ++e) mv[e] = B.mk[16 * (e >> 2) + 4 * (e & 3) + q4];
+      if (tb + TILE <= p.mask_len) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] = fmaf(mv[e], inv_csm, s[e]);
+      } else {
+        const int mlim = (int)max<int64_t>(p.mask_len - tb, 0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int key = 16 * (e >> 2) + 4 * (e & 3) + q4;
+          s[e] = key < mlim ? fmaf(mv[e], inv_csm, s[e]) : -INFINITY;
+        }
       }
     }
     if (tb + TILE > w1) {  // keys past this wave's range: no score, no value scale
@@ -434,13 +461,13 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   // (unrolled by 3 so that each ring position is its own LDS object; a 4th buffer, the whole
   // 160 KB of LDS per CU at 2 workgroups, measured no faster)
   for (int tb = w0; tb < w1; tb += 3 * TILE) {
-    if (tb + 2 * TILE < w1) issue_tile<G>(R, tb + 2 * TILE, S, tiles2[wave], lane);
+    if (tb + 2 * TILE < w1) issue_tile<G, MASK>(R, tb + 2 * TILE, S, tiles2[wave], lane);
     process(tb, tiles0[wave]);
     if (tb + TILE >= w1) break;
-    if (tb + 3 * TILE < w1) issue_tile<G>(R, tb + 3 * TILE, S, tiles0[wave], lane);
+    if (tb + 3 * TILE < w1) issue_tile<G, MASK>(R, tb + 3 * TILE, S, tiles0[wave], lane);
     process(tb + TILE, tiles1[wave]);
     if (tb + 2 * TILE >= w1) break;
-    if (tb + 4 * TILE < w1) issue_tile<G>(R, tb + 4 * TILE, S, tiles1[wave], lane);
+    if (tb + 4 * TILE < w1) issue_tile<G, MASK>(R, tb + 4 * TILE, S, tiles1[wave], lane);
     process(tb + 2 * TILE, tiles2[wave]);
   }
 
@@ -534,6 +561,11 @@ bool fast_path_ok(const AttnParams& p) {
   if (((uintptr_t)p.ks & 3) != 0 || ((uintptr_t)p.vs & 3) != 0) return false;
   // buffer sizes of one (batch, KV head) block are 32-bit
   if (p.S * 64 >= ((int64_t)1 << 31)) return false;
+  // the mask row loads per lane with a 32-bit key stride and a 32-bit extent
+  if (p.mask != nullptr) {
+    if (p.mask_sk <= 0 || ((uintptr_t)p.mask & 3) != 0) return false;
+    if (p.mask_len * p.mask_sk * 4 >= ((int64_t)1 << 31)) return false;
+  }
   return true;
 }
 
@@ -552,7 +584,7 @@ static int64_t resident_fast_waves() {
     }
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(&attn_fast_kernel<4, 4>), THREADS, 0) != hipSuccess ||
+            &per_cu, reinterpret_cast<const void*>(&attn_fast_kernel<4, 4, false>), THREADS, 0) != hipSuccess ||
         per_cu <= 0) {
       per_cu = 2;
     }
@@ -577,8 +609,12 @@ SplitPlan plan_fast(int64_t B, int64_t Hkv, int64_t S) {
 
 template <int NREP, int G>
 static void launch_one(const AttnParams& p, hipStream_t st) {
-  hipLaunchKernelGGL((attn_fast_kernel<NREP, G>), dim3((unsigned)(p.B * p.Hkv), (unsigned)p.nsplit),
-                     dim3(THREADS), 0, st, p);
+  const dim3 grid((unsigned)(p.B * p.Hkv), (unsigned)p.nsplit);
+  if (p.mask != nullptr) {
+    hipLaunchKernelGGL((attn_fast_kernel<NREP, G, true>), grid, dim3(THREADS), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((attn_fast_kernel<NREP, G, false>), grid, dim3(THREADS), 0, st, p);
+  }
 }
 
 int launch_fast(const AttnParams& p, hipStream_t st) {
