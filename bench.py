@@ -220,6 +220,7 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
     hq, hkv, d, g = 32, 8, 128, 32
     shapes = [(B, S, g) for B in (1, 8, 64) for S in (1024, 4096, 16384)]
     shapes.append((8, 2072, 64))  # the shape of the reference's own published figure (A100)
+    shapes.append((64, 16384, 64))  # the reference driver's default group (--kv-group-size 64)
     for B, S, gs in (shapes if which in ("all", "attention") else ()):
         kp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
         vp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
