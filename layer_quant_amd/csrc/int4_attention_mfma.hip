@@ -27,8 +27,12 @@
 // P V. A = V^T: 16 dims x 32 keys, B = P' with P'[key][(m, h)] = p[key][h] * vscale[key][m].
 // Lane (q, c) reads dword c of key rows q + 4e (e = 0..7) from LDS, so MFMA k (k = 0..7) covers
 // dims 8c + k; the output column (m, h) is kept only for dims of group m. P' is split into bf16
-// hi + lo (two MFMAs, about 16 significant bits). The value offset 136 of the V decode is removed
-// at the end with sum_keys P' from one more MFMA against a ones operand.
+// hi + lo (two MFMAs, about 16 significant bits). Value nibbles decode into the top four mantissa
+// bits of bf16 16.0, i.e. the value 24 + n, and the offset 24 is removed at the end with
+// sum_keys P' from one more MFMA against a ones operand. The accumulators round at the magnitude
+// of 24 * sum P' rather than of the result; decoded as 136 + n (the key decode above) the values
+// gave an error about 5x larger, which dominated the kernel's error on outlier-channel data (a
+// CPU emulation of both decodes, checked against the kernel on the same inputs, gave the ratio).
 #include <math.h>
 #include <stdlib.h>
 
@@ -66,6 +70,13 @@ __device__ __forceinline__ f32x4_t mfma_bf16(u32x4_t a, u32x4_t b, f32x4_t c) {
 // v_bitop3_b32 on gfx950.
 __device__ __forceinline__ uint32_t nib_pair(uint32_t x) {
   return ((x ^ 0x00080008u) & NIB2) | 0x43004300u;
+}
+
+// One bf16 pair from two nibbles of x placed at bits 6:3 and 22:19: the nibble xor 8 in the top
+// four mantissa bits of bf16 16.0, i.e. the value 24 + n (one v_bitop3_b32 after the shift that
+// places the nibbles).
+__device__ __forceinline__ uint32_t nib_pair_top(uint32_t x) {
+  return ((x ^ 0x00400040u) & 0x00780078u) | 0x41804180u;
 }
 
 // 8 nibbles of one dword -> bf16 values 136 + n, in the slot order of dims (0, 4, 1, 5, 2, 6, 3, 7).
@@ -352,10 +363,12 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
       for (int u = 0; u < 4; ++u) {
         const uint32_t ylo = __builtin_amdgcn_perm(vw[2 * u + 1], vw[2 * u], 0x05040100u);
         const uint32_t yhi = __builtin_amdgcn_perm(vw[2 * u + 1], vw[2 * u], 0x07060302u);
+        va[0][u] = nib_pair_top(ylo << 3);
+        va[4][u] = nib_pair_top(yhi << 3);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          va[j][u] = nib_pair(ylo >> (4 * j));
-          va[4 + j][u] = nib_pair(yhi >> (4 * j));
+        for (int j = 1; j < 4; ++j) {
+          va[j][u] = nib_pair_top(ylo >> (4 * j - 3));
+          va[4 + j][u] = nib_pair_top(yhi >> (4 * j - 3));
         }
       }
       // keep the decode here: without this the compiler sinks it past the softmax branches to
@@ -486,7 +499,7 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
     for (int k = 0; k < 8; ++k) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        ow[colh * FAST_D + 32 * q4 + 8 * r + k] = acc[k][r] - 136.0f * corr[r];
+        ow[colh * FAST_D + 32 * q4 + 8 * r + k] = acc[k][r] - 24.0f * corr[r];
       }
     }
   }

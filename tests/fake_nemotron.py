@@ -4,9 +4,12 @@ It has just the surface that the reference's patch / register functions touch:
 model.backbone.layers[i].{block_type, mixer, norm, residual_in_fp32}; attention mixers with
 q/k/v/o projections, num_heads, head_dim, num_key_value_heads, num_key_value_groups,
 hidden_size, layer_idx, attention_dropout; Mamba mixers with num_heads, head_dim,
-ssm_state_size whose decode step calls the module-level `selective_state_update` (looked up at
-call time, so rebinding it takes effect); module-level `repeat_kv` and
-`HybridMambaAttentionDynamicCache`. Weights are random; nothing here is the real model.
+ssm_state_size whose decode step (one token with a cache) calls the module-level
+`selective_state_update` (looked up at call time, so rebinding it takes effect) on the cache's
+own [B, H, P, N] state tensor, as the remote module does, so an id()-keyed registry finds it;
+module-level `repeat_kv` and `HybridMambaAttentionDynamicCache`. A remote module imported
+without mamba-ssm has `selective_state_update = None`; tests emulate that by setting it to
+None before patching. Weights are random; nothing here is the real model.
 """
 from __future__ import annotations
 
@@ -60,7 +63,7 @@ class HybridMambaAttentionDynamicCache:
         for kind in config.hybrid_override_pattern:
             if kind == "M":
                 self.ssm_states.append(torch.zeros(
-                    batch_size, config.mamba_num_heads * config.mamba_head_dim,
+                    batch_size, config.mamba_num_heads, config.mamba_head_dim,
                     config.ssm_state_size, dtype=dtype, device=device))
             else:
                 self.ssm_states.append(torch.zeros(0, device=device))
@@ -125,31 +128,44 @@ class FakeMamba(nn.Module):
         self.D = nn.Parameter(torch.randn(self.num_heads))
         self.dt_bias = nn.Parameter(torch.randn(self.num_heads) * 0.1)
 
-    def forward(self, hidden_states, cache_params=None, cache_position=None, attention_mask=None):
-        bsz = hidden_states.shape[0]
+    def _step_args(self, proj):
+        bsz = proj.shape[0]
         inner = self.num_heads * self.head_dim
         gn = self.n_groups * self.ssm_state_size
-        x, B, C, dt = torch.split(self.in_proj(hidden_states[:, -1]), [inner, gn, gn, self.num_heads],
-                                  dim=-1)
-        if cache_params is None:
-            state = torch.zeros(bsz, inner, self.ssm_state_size, device=hidden_states.device)
-        else:
-            state = cache_params.ssm_states[self.layer_idx]
-        ssm_update = globals()["selective_state_update"]
-        y = ssm_update(
-            state.view(bsz, self.num_heads, self.head_dim, self.ssm_state_size),
-            x.reshape(bsz, self.num_heads, self.head_dim),
-            dt[:, :, None].expand(-1, -1, self.head_dim),
-            (-torch.exp(self.A_log.float()))[:, None, None].expand(-1, self.head_dim,
-                                                                  self.ssm_state_size),
-            B.reshape(bsz, self.n_groups, self.ssm_state_size),
-            C.reshape(bsz, self.n_groups, self.ssm_state_size),
-            self.D[:, None].expand(-1, self.head_dim),
-            z=None,
-            dt_bias=self.dt_bias[:, None].expand(-1, self.head_dim),
-            dt_softplus=True,
-        )
-        return self.out_proj(y.reshape(bsz, 1, inner))
+        x, B, C, dt = torch.split(proj, [inner, gn, gn, self.num_heads], dim=-1)
+        return (x.reshape(bsz, self.num_heads, self.head_dim),
+                dt[:, :, None].expand(-1, -1, self.head_dim),
+                (-torch.exp(self.A_log.float()))[:, None, None].expand(-1, self.head_dim,
+                                                                      self.ssm_state_size),
+                B.reshape(bsz, self.n_groups, self.ssm_state_size),
+                C.reshape(bsz, self.n_groups, self.ssm_state_size),
+                self.D[:, None].expand(-1, self.head_dim),
+                self.dt_bias[:, None].expand(-1, self.head_dim))
+
+    def forward(self, hidden_states, cache_params=None, cache_position=None, attention_mask=None):
+        bsz, seq_len, _ = hidden_states.shape
+        inner = self.num_heads * self.head_dim
+        proj = self.in_proj(hidden_states)
+        if cache_params is not None and seq_len == 1:
+            # decode: the (possibly rebound) module-level update on the cache's own state object
+            x, dt, A, B, C, D, dt_bias = self._step_args(proj[:, 0])
+            ssm_update = globals()["selective_state_update"]
+            y = ssm_update(cache_params.ssm_states[self.layer_idx], x, dt, A, B, C, D, z=None,
+                           dt_bias=dt_bias, dt_softplus=True)
+            return self.out_proj(y.reshape(bsz, 1, inner))
+        # prefill (the remote module's chunked scan): the same recurrence token by token in
+        # fp32, leaving the final state in the cache
+        state = torch.zeros(bsz, self.num_heads, self.head_dim, self.ssm_state_size,
+                            device=hidden_states.device)
+        ys = []
+        for t in range(seq_len):
+            x, dt, A, B, C, D, dt_bias = self._step_args(proj[:, t])
+            ys.append(_torch_selective_state_update(state, x, dt, A, B, C, D, dt_bias=dt_bias,
+                                                    dt_softplus=True))
+        if cache_params is not None:
+            cache_params.ssm_states[self.layer_idx].copy_(state)
+        y = torch.stack(ys, dim=1)
+        return self.out_proj(y.reshape(bsz, seq_len, inner))
 
 
 class FakeMLP(nn.Module):
@@ -206,20 +222,24 @@ class FakeNemotronHForCausalLM(nn.Module):
     def device(self):
         return self.lm_head.weight.device
 
-    def forward(self, input_ids, cache_params=None, cache_position=None, attention_mask=None):
+    def forward(self, input_ids, cache_params=None, cache_position=None, attention_mask=None,
+                use_cache=False, return_dict=False):
         h = self.backbone.embeddings(input_ids)
         for layer in self.backbone.layers:
             h = layer(h, cache_params=cache_params, cache_position=cache_position,
                       attention_mask=attention_mask).to(self.lm_head.weight.dtype)
-        return self.lm_head(h)
+        logits = self.lm_head(h)
+        return SimpleNamespace(logits=logits) if return_dict else logits
+
+
+_torch_selective_state_update = selective_state_update
 
 
 def reset_module():
-    """Undo every attribute the patch functions set on this module."""
+    """Undo every attribute the patch functions set on this module (and a None
+    selective_state_update set by a test)."""
     g = globals()
-    original = g.get("_mx_state_kernel_original")
-    if original is not None:
-        g["selective_state_update"] = original
+    g["selective_state_update"] = _torch_selective_state_update
     for name in ("_mx_state_kernel_original", "_mx_state_kernel_patched",
                  "_mx_state_kernel_stochastic", "_mx_state_kernel_seed",
                  "_mamba_decode_state_kernel_caches"):

@@ -209,11 +209,49 @@ def test_attention_long_wave_ranges_ragged_tail(gpu, s, g):
     assert_close_rel(_run_attention(gpu, cache, q, s, nrep, g), ref, what="fast")
 
 
-@pytest.mark.parametrize("b,hkv,nrep,s,g", [(64, 8, 4, 4096, 32), (8, 8, 4, 4133, 32),
-                                             (16, 8, 4, 2999, 64), (2, 2, 16, 777, 128)])
-def test_attention_repeats_bit_identical(gpu, b, hkv, nrep, s, g):
+def _long_range_masks(b, s):
+    """Masks for B=64 at S ~ 1000, where each wave of the MFMA path walks 256 keys (8 tiles):
+    a keep-mask whose left padding covers a whole wave's range and part of the next (rows 0-7:
+    300-307 keys), padding inside one tile and a gap across a tile edge in other rows; a 4-D
+    additive bias; and a short bias mask that ends inside the third wave's range and inside a
+    tile (700 keys)."""
+    gen = torch.Generator().manual_seed(s)
+    keep = torch.ones(b, s, dtype=torch.bool)
+    for r in range(8):
+        keep[r, :300 + r] = False
+    keep[8:16, :17] = False
+    keep[16:24, 500:540] = False
+    keep[24, s - 1] = False
+    return {
+        "keep": oik.decode_attention_mask(keep, b, s),
+        "bias": oik.decode_attention_mask(torch.randn(b, 1, 1, s, generator=gen) * 3, b, s),
+        "short": torch.randn(b, 1, 1, 700, generator=gen),
+    }
+
+
+@pytest.mark.parametrize("s,g", [(999, 32), (1057, 64), (1150, 128)])
+def test_attention_long_wave_ranges_masked(gpu, s, g):
+    """The masked MFMA instance (7 LDS-direct loads per tile) through the whole 3-buffer ring and
+    the ragged last tile of each ring position, with masks that end or open inside a wave."""
+    b, hkv, nrep, d = 64, 8, 4, 128
+    cache = _packed_cache(b, hkv, s, d, g, 1400 + s, cap=s + 5)
+    q = _activations((b, hkv * nrep, 1, d), 1450 + s, torch.bfloat16)
+    for name, mask in _long_range_masks(b, s).items():
+        ref = oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
+                                   cache["v_scale"], s, nrep, g, mask=mask)
+        assert_close_rel(_run_attention(gpu, cache, q, s, nrep, g, mask=mask), ref, what=name)
+
+
+@pytest.mark.parametrize("b,hkv,nrep,s,g,masked", [(64, 8, 4, 4096, 32, False),
+                                                   (8, 8, 4, 4133, 32, False),
+                                                   (16, 8, 4, 2999, 64, False),
+                                                   (2, 2, 16, 777, 128, False),
+                                                   (64, 8, 4, 1057, 64, True),
+                                                   (8, 8, 4, 4133, 32, True)])
+def test_attention_repeats_bit_identical(gpu, b, hkv, nrep, s, g, masked):
     """The MFMA path's tile loads land in LDS behind explicit waits: repeated calls on the same
-    inputs must give bit-identical outputs (a missing or short wait would read a tile early)."""
+    inputs must give bit-identical outputs (a missing or short wait would read a tile early).
+    The masked instance counts 7 loads per tile in its waits."""
     d = 128
     gen = torch.Generator(device=gpu).manual_seed(b * 7 + s)
     kp = torch.randint(0, 256, (b, hkv, s, d // 2), dtype=torch.uint8, device=gpu, generator=gen)
@@ -221,12 +259,16 @@ def test_attention_repeats_bit_identical(gpu, b, hkv, nrep, s, g):
     ks = torch.rand(b, hkv, s, d // g, device=gpu, generator=gen) + 0.01
     vs = torch.rand(b, hkv, s, d // g, device=gpu, generator=gen) + 0.01
     q = torch.randn(b, hkv * nrep, 1, d, device=gpu, generator=gen).to(torch.bfloat16)
+    mask = None
+    if masked:
+        mask = (torch.randn(b, 1, 1, s, device=gpu, generator=gen) * 2).contiguous()
+        mask[:, :, :, :300] = float("-inf")
     ref = torch.empty(b, hkv * nrep, d, device=gpu)
-    _abi.int4_decode_attention(q, kp, vp, ks, vs, None, ref, s, nrep, g)
+    _abi.int4_decode_attention(q, kp, vp, ks, vs, mask, ref, s, nrep, g)
     out = torch.empty_like(ref)
     for _ in range(20):
         out.fill_(float("nan"))
-        _abi.int4_decode_attention(q, kp, vp, ks, vs, None, out, s, nrep, g)
+        _abi.int4_decode_attention(q, kp, vp, ks, vs, mask, out, s, nrep, g)
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
     assert torch.isfinite(ref).all()
