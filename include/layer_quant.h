@@ -10,7 +10,9 @@
  *
  * Conventions
  *   - The caller owns every buffer. The library never allocates device memory; scratch space
- *     (split-K partials) comes from a caller workspace sized by a query function.
+ *     (split-K partials) comes from a caller workspace sized by a query function, or, for
+ *     lq_int4_decode_attention_noalloc, from a static 8 MiB buffer per device that the library's
+ *     code object holds from load to process end.
  *   - Every launch is asynchronous on the caller's HIP stream, passed as `void* stream`
  *     (a hipStream_t; NULL is the legacy default stream). No entry point synchronizes.
  *   - Tensors are described by lq_tensor: a device pointer, a dtype code, a rank (1..4), a shape
@@ -132,6 +134,28 @@ int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
                              const lq_tensor* v_scale, const lq_tensor* mask, const lq_tensor* out,
                              int64_t seq_len, int num_key_value_groups, int group_size,
                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * lq_int4_decode_attention without a workspace: the same validation, kernels and results, with
+ * the split-K partials in a static per-device buffer inside the library
+ * (LQ_DECODE_ATTENTION_NOALLOC_SCRATCH_BYTES, 8 MiB on every GPU the library runs on, held until
+ * the process ends). At 32 query / 8 KV heads and head_dim 128 any batch and context needs at
+ * most 2 MiB of it; rarer shapes that need more (16 query heads per KV head, or head_dim 512, at
+ * some batch sizes) get LQ_ERR_WORKSPACE (lq_int4_decode_attention_workspace gives the size a
+ * shape needs). Calls no allocating routine.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Every call on one GPU shares that GPU's buffer and it keeps the last call's partials (nothing
+ * in it has to start at zero): calls that overlap on one GPU -- on different streams, or from
+ * different host threads -- race and must be serialized by the caller; calls in order on one
+ * stream are safe. The buffer is on the device that runs `stream`.
+ */
+#define LQ_DECODE_ATTENTION_NOALLOC_SCRATCH_BYTES (8u << 20)
+int lq_int4_decode_attention_noalloc(const lq_tensor* q, const lq_tensor* k_packed,
+                                     const lq_tensor* v_packed, const lq_tensor* k_scale,
+                                     const lq_tensor* v_scale, const lq_tensor* mask,
+                                     const lq_tensor* out, int64_t seq_len,
+                                     int num_key_value_groups, int group_size, void* stream);
 
 /*
  * Causal INT4 prefill attention over the packed cache: query position t of q [B, Hq, L, D]

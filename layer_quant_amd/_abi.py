@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "lq_int4_pack_kv_pair",
     "lq_int4_decode_attention_workspace",
     "lq_int4_decode_attention",
+    "lq_int4_decode_attention_noalloc",
     "lq_int4_prefill_attention",
     "lq_mx_encode",
     "lq_mx_decode",
@@ -91,6 +92,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.lq_int4_decode_attention.argtypes = [_P] * 7 + [
         ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
         ctypes.c_void_p]
+    lib.lq_int4_decode_attention_noalloc.restype = ctypes.c_int
+    lib.lq_int4_decode_attention_noalloc.argtypes = [_P] * 7 + [
+        ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     lib.lq_int4_prefill_attention.restype = ctypes.c_int
     lib.lq_int4_prefill_attention.argtypes = [_P] * 6 + [ctypes.c_int, ctypes.c_int,
                                                           ctypes.c_void_p]
@@ -241,6 +245,22 @@ def int4_decode_attention(q: torch.Tensor, k_packed: torch.Tensor, v_packed: tor
         desc(out), int(seq_len), int(num_key_value_groups), int(group_size),
         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream)
     check(rc, "lq_int4_decode_attention")
+    return out
+
+
+def int4_decode_attention_noalloc(q: torch.Tensor, k_packed: torch.Tensor,
+                                  v_packed: torch.Tensor, k_scale: torch.Tensor,
+                                  v_scale: torch.Tensor, mask: torch.Tensor | None,
+                                  out: torch.Tensor, seq_len: int, num_key_value_groups: int,
+                                  group_size: int) -> torch.Tensor:
+    """int4_decode_attention with the split-K partials in the library's static per-device
+    scratch: allocates nothing (for callers that cannot allocate). Calls overlapping on one GPU
+    share that scratch and race."""
+    dev = _require_gpu(q, k_packed, v_packed, k_scale, v_scale, mask, out)
+    rc = lib().lq_int4_decode_attention_noalloc(
+        desc(q), desc(k_packed), desc(v_packed), desc(k_scale), desc(v_scale), desc(mask),
+        desc(out), int(seq_len), int(num_key_value_groups), int(group_size), _stream(dev))
+    check(rc, "lq_int4_decode_attention_noalloc")
     return out
 
 

@@ -11,6 +11,9 @@
 // the caller's workspace and attn_merge_kernel combines them; a single split writes out directly.
 #include <math.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "int4_attention.h"
 
 namespace lq {
@@ -235,6 +238,63 @@ static void carve_workspace(AttnParams& p, void* ws) {
   p.ws_acc = (float*)(base + 2 * ml);
 }
 
+// Split-K partials of lq_int4_decode_attention_noalloc: a static buffer on every device the
+// library runs on, held until the process ends. 8 MiB: at 32 q / 8 KV heads, head_dim 128 any
+// batch and context needs at most 2.0 MiB; larger needs (16 q heads per KV head, or head_dim
+// 512, at some batch sizes) are rejected. In host code `scratch` names a host-side stand-in,
+// never the device memory: the device address comes from hipGetSymbolAddress, once per device
+// (scratch_address).
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)LQ_DECODE_ATTENTION_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::atomic<void*> scratch_ptr[MAX_DEVICES];
+static std::mutex scratch_mutex;
+
+// Device address of `scratch` on the device that runs `stream` (the current device for the
+// legacy NULL stream), looked up on the first call for that device with the device made current.
+static int scratch_address(hipStream_t stream, void** out) {
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) return fail(LQ_ERR_HIP, "hipGetDevice failed");
+  int dev = cur;
+  if (stream != nullptr && hipStreamGetDevice(stream, &dev) != hipSuccess) {
+    return fail(LQ_ERR_HIP, "hipStreamGetDevice failed");
+  }
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(LQ_ERR_HIP, "device %d out of range", dev);
+  void* ptr = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    ptr = scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      if (dev != cur && hipSetDevice(dev) != hipSuccess) {
+        return fail(LQ_ERR_HIP, "hipSetDevice(%d) failed", dev);
+      }
+      const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (dev != cur) (void)hipSetDevice(cur);
+      if (e != hipSuccess || ptr == nullptr) {
+        return fail(LQ_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                    hipGetErrorString(e));
+      }
+      scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return LQ_OK;
+}
+
+// Where the split-K partials go: the caller's workspace, or the static per-device scratch.
+struct PartialsBuffer {
+  void* workspace;
+  size_t workspace_bytes;
+  bool use_scratch;
+};
+
+static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
+                            const lq_tensor* v_packed, const lq_tensor* k_scale,
+                            const lq_tensor* v_scale, const lq_tensor* mask, const lq_tensor* out,
+                            int64_t seq_len, int num_key_value_groups, int group_size,
+                            PartialsBuffer buf, void* stream);
+
 }  // namespace lq
 
 using namespace lq;
@@ -258,6 +318,30 @@ extern "C" int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_p
                                         const lq_tensor* out, int64_t seq_len,
                                         int num_key_value_groups, int group_size,
                                         void* workspace, size_t workspace_bytes, void* stream) {
+  return decode_attention(q, k_packed, v_packed, k_scale, v_scale, mask, out, seq_len,
+                          num_key_value_groups, group_size,
+                          PartialsBuffer{workspace, workspace_bytes, false}, stream);
+}
+
+extern "C" int lq_int4_decode_attention_noalloc(const lq_tensor* q, const lq_tensor* k_packed,
+                                                const lq_tensor* v_packed,
+                                                const lq_tensor* k_scale,
+                                                const lq_tensor* v_scale, const lq_tensor* mask,
+                                                const lq_tensor* out, int64_t seq_len,
+                                                int num_key_value_groups, int group_size,
+                                                void* stream) {
+  return decode_attention(q, k_packed, v_packed, k_scale, v_scale, mask, out, seq_len,
+                          num_key_value_groups, group_size, PartialsBuffer{nullptr, 0, true},
+                          stream);
+}
+
+namespace lq {
+
+static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
+                            const lq_tensor* v_packed, const lq_tensor* k_scale,
+                            const lq_tensor* v_scale, const lq_tensor* mask, const lq_tensor* out,
+                            int64_t seq_len, int num_key_value_groups, int group_size,
+                            PartialsBuffer buf, void* stream) {
   int rc;
   if (q == nullptr) return fail(LQ_ERR_INVALID_ARG, "q: descriptor is NULL");
   const int qdim = q->ndim;
@@ -357,18 +441,29 @@ extern "C" int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_p
   p.nsplit = sp.nsplit;
   p.chunk = sp.chunk;
   const size_t need = partial_bytes(B, Hq, D, p.nsplit);
-  if (need > 0) {
-    if (workspace == nullptr || workspace_bytes < need) {
-      return fail(LQ_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
-                  workspace == nullptr ? (size_t)0 : workspace_bytes);
+  hipStream_t st = (hipStream_t)stream;
+  if (need > 0 && buf.use_scratch) {
+    if (need > NOALLOC_SCRATCH_BYTES) {
+      return fail(LQ_ERR_WORKSPACE,
+                  "lq_int4_decode_attention_noalloc: this shape needs %zu bytes of split-K "
+                  "partials, more than the library's %zu-byte static scratch; call "
+                  "lq_int4_decode_attention with a workspace instead", need,
+                  NOALLOC_SCRATCH_BYTES);
     }
-    if (((uintptr_t)workspace & 255) != 0) {
+    void* ptr = nullptr;
+    if ((rc = scratch_address(st, &ptr)) != LQ_OK) return rc;
+    carve_workspace(p, ptr);
+  } else if (need > 0) {
+    if (buf.workspace == nullptr || buf.workspace_bytes < need) {
+      return fail(LQ_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
+                  buf.workspace == nullptr ? (size_t)0 : buf.workspace_bytes);
+    }
+    if (((uintptr_t)buf.workspace & 255) != 0) {
       return fail(LQ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
     }
-    carve_workspace(p, workspace);
+    carve_workspace(p, buf.workspace);
   }
 
-  hipStream_t st = (hipStream_t)stream;
   if (fast) {
     if ((rc = launch_fast(p, st)) != LQ_OK) return rc;
   } else {
@@ -382,3 +477,5 @@ extern "C" int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_p
   }
   return LQ_OK;
 }
+
+}  // namespace lq
