@@ -1,33 +1,29 @@
-"""WikiText loading for the decode driver (reference hybrid_quant/data.py:14-32).
+"""WikiText text source of the decode driver.
 
-`datasets` is imported on first use, so importing this module needs no network or dataset.
+Interface of reference hybrid_quant/data.py:14-20 (the driver imports only
+`load_wikitext_texts`). `datasets` is imported on first use, so importing this module needs
+neither the package nor a network.
 """
 from __future__ import annotations
 
 from pathlib import Path
-from typing import Iterable, List
 
 from .env import configure_cache_env
 
 configure_cache_env()
 
-
-def load_wikitext_texts(dataset_path: str, split: str = "test") -> List[str]:
-    """Non-blank lines of wikitext-103-raw-v1 from a local dataset directory or hub name."""
-    from datasets import load_dataset
-
-    source = str(Path(dataset_path)) if Path(dataset_path).exists() else dataset_path
-    ds = load_dataset(source, "wikitext-103-raw-v1", split=split)
-    return [text for text in ds["text"] if text and not text.isspace()]
+WIKITEXT_CONFIG = "wikitext-103-raw-v1"
 
 
-def token_segments(tokenizer, texts: Iterable[str], context_length: int, max_eval_tokens: int):
-    """Overlapping windows of context_length + 1 token ids over the joined texts."""
-    ids = tokenizer("\n\n".join(texts), add_special_tokens=False, return_tensors="pt").input_ids[0]
-    usable = min(ids.numel() - 1, max_eval_tokens)
-    start = 0
-    while start < usable:
-        stop = min(start + context_length + 1, usable + 1)
-        if stop - start >= 2:
-            yield ids[start:stop]
-        start = stop - 1
+def load_wikitext_texts(dataset_path: str, split: str = "test") -> list[str]:
+    """Lines of the WikiText-103 (raw) split that hold any non-whitespace character.
+
+    `dataset_path` names a local dataset directory when one exists there, otherwise a dataset
+    known to `datasets.load_dataset`.
+    """
+    import datasets
+
+    where = Path(dataset_path)
+    rows = datasets.load_dataset(str(where) if where.exists() else dataset_path, WIKITEXT_CONFIG,
+                                 split=split)
+    return [line for line in rows["text"] if line.strip()]

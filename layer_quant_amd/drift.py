@@ -44,10 +44,13 @@ def _rel(a: torch.Tensor, b: torch.Tensor) -> float:
 
 def run(batch: int = 8, steps: int = 2048, checkpoints=(128, 256, 512, 1024, 2048),
         seed: int = 0, device: str = "cuda:0", record: dict | None = None,
-        rounding: str = "counter") -> dict:
-    """The experiment; `record`, when given, receives CPU copies of h0, A, D and every step's
-    inputs (for replaying a short chain elsewhere). `rounding` is "counter" (the library's
-    generator) or "uniform" (a uniform tensor per step from the seeded generator)."""
+        rounding: str = "counter", record_states: int = 0,
+        record_steps: int | None = None) -> dict:
+    """The experiment; `record`, when given, receives CPU copies of h0, A, D and the inputs of
+    the first `record_steps` steps (all steps by default) for replaying a short chain elsewhere,
+    and with record_states = k the MX4 and MX8 states (q, shared_exp, micro_exp) after each of
+    the first k steps in record["states"]. `rounding` is "counter" (the library's generator) or
+    "uniform" (a uniform tensor per step from the seeded generator)."""
     if rounding not in ("counter", "uniform"):
         raise ValueError(f"rounding must be 'counter' or 'uniform', got {rounding!r}")
     dev = torch.device(device)
@@ -58,7 +61,7 @@ def run(batch: int = 8, steps: int = 2048, checkpoints=(128, 256, 512, 1024, 204
         HEADS, DIM, DSTATE)
     D = torch.randn(HEADS, device=dev, generator=gen)[:, None].expand(HEADS, DIM)
     if record is not None:
-        record.update(h0=h0.cpu(), A=A.cpu(), D=D.cpu(), steps=[])
+        record.update(h0=h0.cpu(), A=A.cpu(), D=D.cpu(), steps=[], states=[])
 
     mx = {}
     for bits in (4, 8):
@@ -84,7 +87,7 @@ def run(batch: int = 8, steps: int = 2048, checkpoints=(128, 256, 512, 1024, 204
         Bm = torch.randn(batch, GROUPS, DSTATE, device=dev, generator=gen).to(torch.bfloat16)
         Cm = torch.randn(batch, GROUPS, DSTATE, device=dev, generator=gen).to(torch.bfloat16)
         uni = (torch.rand(shape, device=dev, generator=gen) if rounding == "uniform" else None)
-        if record is not None:
+        if record is not None and (record_steps is None or step <= record_steps):
             record["steps"].append(dict(x=x.cpu(), dt=dt.cpu(), B=Bm.cpu(), C=Cm.cpu(),
                                         uniform=None if uni is None else uni.cpu()))
         for bits in (4, 8):
@@ -98,6 +101,8 @@ def run(batch: int = 8, steps: int = 2048, checkpoints=(128, 256, 512, 1024, 204
                                      uniform=uni)
         for name, state in plain.items():
             _abi.selective_state_update(state, x, dt, None, A, Bm, Cm, D, None, outs[name], False)
+        if record is not None and step <= record_states:
+            record["states"].append({bits: tuple(t.cpu() for t in mx[bits]) for bits in (4, 8)})
         if step in marks:
             row = {"step": step}
             for bits in (4, 8):

@@ -37,8 +37,12 @@ for both signs, exact fractions) and its clamp;
 the update's closed forms (dt = 0 leaves h unchanged so the writeback is a pure re-encode;
 A = 0 gives h + dt*B*x; softplus threshold at 20) against an independent float64 evaluation.
 bf16_state_update (drift baseline) restates mamba_ssm's selective_state_update, a dependency
-(mamba-ssm 2.3.2.post1) that is not installed: its arithmetic is update_math (pinned above); bit
-parity with mamba-ssm's Triton kernel is unpinned.
+(mamba-ssm 2.3.2.post1) that is not installed. It is pinned (tests/test_oracle_bf16_state.py) in
+fp32 against an independent implementation of the same semantics that is installed:
+transformers' modeling_nemotron_h.mamba2_selective_state_update (dt_bias, softplus with the
+identity above 20, the decay/input update and the silu(z) gate); its bf16 store by torch's
+round-to-nearest-even conversion. Only bit parity with mamba-ssm's own Triton kernel (its
+approximate exp and operation order) stays unpinned.
 
 Compact layout (this build's opt-in cache layout, no reference counterpart): to_compact /
 from_compact convert the reference layout to micro-exponent bits (bit k of byte j = pair 8j + k

@@ -27,3 +27,14 @@ def gpu():
 def pytest_runtest_setup(item):
     if item.get_closest_marker("gpu") is not None:
         print(f"\n[gpu-test] {item.nodeid}", flush=True)
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Measurements that GPU tests register in helpers.REPORT (e.g. the config-4 drift table),
+    printed after the run so that they appear next to the final result line."""
+    import helpers
+
+    if helpers.REPORT:
+        terminalreporter.section("measurements")
+        for line in helpers.REPORT:
+            terminalreporter.write_line(line)

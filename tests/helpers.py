@@ -6,6 +6,9 @@ import torch
 
 RTOL = 2e-3  # the attention output / updated state tolerance, fp32 accumulation
 
+# lines that tests register for the session's terminal summary (conftest.py prints them)
+REPORT: list[str] = []
+
 
 def assert_close_rel(out: torch.Tensor, ref: torch.Tensor, rtol: float = RTOL, what: str = ""):
     """|out - ref| <= rtol * (|ref| + mean|ref|) elementwise, and the relative Frobenius error

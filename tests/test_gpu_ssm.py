@@ -4,6 +4,7 @@ against the oracle's fp32 restatement: y within 2e-3; the stored state equal to 
 after rounding to the state dtype for >= 99.9% of elements and within one unit in the last place
 elsewhere (the kernel's fma rounds once where the oracle rounds twice); dt = 0 leaves the state
 bit-identical."""
+import numpy as np
 import pytest
 import torch
 
@@ -207,3 +208,70 @@ def test_drift_tool_replays_on_the_oracle(gpu, rounding):
         for k, v in ref.items():
             assert np.isfinite(row[k])
             assert abs(row[k] - v) <= 0.05 * v + 1e-6, (row["step"], k, row[k], v)
+
+
+def _replay_slices(rec, bits, steps, slices):
+    """The oracle's update of each recorded MX state, one step at a time from the GPU's own
+    state before the step, on (batch, group) slices (rows are independent and the uniform
+    tensor is per element, so a slice replays exactly)."""
+    from helpers import assert_mx_writeback, update_term_magnitudes
+
+    hpg = 128 // 8
+    prev = omx.mx_encode(rec["h0"].numpy(), bits, omx.ROUND_NEAREST_EVEN)
+    for i in range(steps):
+        s = rec["steps"][i]
+        got = [t.numpy() for t in rec["states"][i][bits]]
+        for b, g in slices:
+            bs, hs = slice(b, b + 1), slice(g * hpg, (g + 1) * hpg)
+            q, e, m = (a[bs, hs] for a in prev)
+            args = (s["x"][bs, hs], s["dt"][bs, hs], rec["A"][hs], s["B"][bs, g:g + 1],
+                    s["C"][bs, g:g + 1])
+            uni = s["uniform"][bs, hs]
+            rq, re_, rm, _, rh = omx.mx_update(q, e, m, *args, D=rec["D"][hs], format_bits=bits,
+                                               round_mode=omx.ROUND_SR_UNIFORM, uniform=uni)
+            mag = update_term_magnitudes(omx.mx_decode(q, e, m), *args)
+            assert_mx_writeback([a[bs, hs] for a in got], (rq, re_, rm), rh, mag, bits,
+                                omx.ROUND_SR_UNIFORM, uniform=uni,
+                                what=f"mx{bits} step {i + 1} b{b} g{g}")
+        prev = got
+
+
+@pytest.mark.timeout(300)
+def test_config4_chain_2048_steps(gpu):
+    """one Nemotron-H Mamba2 layer at batch 8 run for 2048 decode steps in
+    MX4 and MX8 next to a bf16 and an fp32 state (layer_quant_amd.drift), with the
+    configuration's own rounding (a seeded uniform tensor per step) and with the counter
+    generator. Checks: every figure finite; MX8 drift below MX4's at every checkpoint; no growth
+    of the MX4 state drift from step 128 to 2048 beyond +-15%; the bf16 state within 1% of
+    fp32; and the first 16 steps of the uniform run replayed through the oracle from the GPU's
+    state before each step on four (batch, group) slices, equal except at encoder decision
+    ties. The checkpoint table is printed in the session's terminal summary."""
+    import json
+
+    from helpers import REPORT
+    from layer_quant_amd import drift
+
+    marks = (128, 256, 512, 1024, 2048)
+    for rounding in ("uniform", "counter"):
+        rec = {}
+        res = drift.run(batch=8, steps=2048, checkpoints=marks, rounding=rounding,
+                        record=rec if rounding == "uniform" else None,
+                        record_states=16, record_steps=16)
+        rows = res["drift"]
+        assert [r["step"] for r in rows] == list(marks)
+        REPORT.append(f"config 4 drift, batch 8, {rounding} rounding "
+                      f"({res['seconds']} s on the GPU): " + json.dumps(
+                          [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()
+                            if k in ("step", "mx4_state_vs_bf16", "mx4_y_vs_bf16",
+                                     "mx8_state_vs_bf16", "mx8_y_vs_bf16",
+                                     "bf16_state_vs_fp32")} for r in rows]))
+        for r in rows:
+            assert all(np.isfinite(v) for v in r.values()), r
+            assert r["mx8_state_vs_bf16"] < r["mx4_state_vs_bf16"], r
+            assert r["mx8_y_vs_bf16"] < r["mx4_y_vs_bf16"], r
+            assert r["bf16_state_vs_fp32"] < 0.01, r
+        d = [r["mx4_state_vs_bf16"] for r in rows]
+        assert max(d) / min(d) <= 1.15 and abs(d[-1] / d[0] - 1) <= 0.15, d
+        if rounding == "uniform":
+            for bits in (4, 8):
+                _replay_slices(rec, bits, 16, [(0, 0), (7, 7), (3, 2), (5, 5)])

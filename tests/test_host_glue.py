@@ -189,5 +189,36 @@ def test_register_rejects_unknown_mode(model):
 def test_mx_constants():
     assert (ms.MX8_BLOCK_SIZE, ms.MX8_PAIR_SIZE, ms.MX8_MANTISSA_MAX) == (16, 2, 63.0)
     assert (ms.MX4_BLOCK_SIZE, ms.MX4_PAIR_SIZE, ms.MX4_MANTISSA_MAX) == (16, 2, 7.0)
-    assert ms.mx8_state_selective_update.__doc__ is None or True
     assert math.isclose(ms.MX4_MANTISSA_MAX, 7)
+
+
+def test_mx8_mx4_aliases_forward_every_argument(monkeypatch):
+    """mx8_/mx4_state_selective_update (ms.py:724-729) call mx_state_selective_update with the
+    caller's positional and keyword arguments unchanged."""
+    seen = []
+    monkeypatch.setattr(ms, "mx_state_selective_update",
+                        lambda *a, **k: seen.append((a, k)) or "y")
+    assert ms.mx8_state_selective_update(1, 2, D=3, stochastic=False) == "y"
+    assert ms.mx4_state_selective_update("c", seed=9) == "y"
+    assert seen == [((1, 2), {"D": 3, "stochastic": False}), (("c",), {"seed": 9})]
+
+
+def test_load_wikitext_texts_filters_blank_lines(monkeypatch, tmp_path):
+    """The driver's text source keeps the non-whitespace lines of the split and passes a local
+    directory as a path, anything else as a dataset name (reference data.py:14-20)."""
+    import sys
+    import types
+
+    from hybrid_quant import data
+
+    calls = []
+
+    def load_dataset(source, config, split):
+        calls.append((source, config, split))
+        return {"text": ["a", "", "  \n", " b ", "\n"]}
+
+    monkeypatch.setitem(sys.modules, "datasets", types.SimpleNamespace(load_dataset=load_dataset))
+    assert data.load_wikitext_texts("wikitext") == ["a", " b "]
+    assert data.load_wikitext_texts(str(tmp_path), split="validation") == ["a", " b "]
+    assert calls == [("wikitext", "wikitext-103-raw-v1", "test"),
+                     (str(tmp_path), "wikitext-103-raw-v1", "validation")]
