@@ -40,7 +40,7 @@ def log(msg: str) -> None:
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=16384)
@@ -51,6 +51,11 @@ def parse_args():
     ap.add_argument("--state-layout", default="reference", choices=["reference", "compact"],
                     help="MX cache layout: the reference's tensors (default) or the compact one "
                          "(bit micro-exponents, MX4 nibble mantissas; same arithmetic)")
+    ap.add_argument("--settle-seconds", type=float, default=0.3,
+                    help="after the warmup steps, keep running untimed steps until this much "
+                         "time has passed: under sustained load the GPU clocks ramp up over the "
+                         "first ~50 ms, and the VALU-heavy MX update runs 20-25 %% slower "
+                         "before they settle")
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--sweep", nargs="?", const="all", default=None,
                     choices=["all", "attention", "state", "prefill"],
@@ -59,6 +64,17 @@ def parse_args():
                          "bf16 state updates: batch 1/8/64; INT4 prefill: L 1K/4K/16K), each call "
                          "after a 512 MB scratch read so that nothing is cache-resident; prints "
                          "one JSON line. An argument restricts it to one kernel family")
+    ap.add_argument("--batches", default=None,
+                    help="--sweep: comma-separated batch sizes to keep (default: all)")
+    ap.add_argument("--ctxs", default=None,
+                    help="--sweep attention: comma-separated contexts to keep (default: all)")
+    ap.add_argument("--lengths", default=None,
+                    help="--sweep prefill: comma-separated prompt lengths (default 1024,4096,16384)")
+    ap.add_argument("--reps", type=int, default=20,
+                    help="--sweep: timed calls per configuration (median reported)")
+    ap.add_argument("--cpu-pairs", choices=["on", "off"], default="on",
+                    help="--sweep: time the CPU oracle on the same inputs next to each "
+                         "attention (batch 1 and 8) and MX-update configuration")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy, the reference kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -72,20 +88,106 @@ class Events:
         self.torch = torch
         self.pairs: dict[str, list] = {}
 
-    def around(self, name, fn):
+    def around(self, name, fn, calls: int = 1):
+        """Time fn() (which makes `calls` launches of kernel `name`, back to back) with one
+        event pair; its launches count as `calls` calls of equal duration."""
         t = self.torch
         a = t.cuda.Event(enable_timing=True)
         b = t.cuda.Event(enable_timing=True)
         a.record()
         fn()
         b.record()
-        self.pairs.setdefault(name, []).append((a, b))
+        self.pairs.setdefault(name, []).append((a, b, calls))
 
     def mean_us(self, name):
         pairs = self.pairs.get(name, [])
         if not pairs:
             return None
-        return 1000.0 * sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
+        return 1000.0 * sum(a.elapsed_time(b) for a, b, _ in pairs) / sum(c for *_, c in pairs)
+
+    def spread_us(self, name):
+        """min / median / max of the per-call durations (us; per event pair divided by its
+        launches) and the number of calls."""
+        pairs = self.pairs.get(name, [])
+        us = sorted(1000.0 * a.elapsed_time(b) / c for a, b, c in pairs)
+        if not us:
+            return None
+        return {"min": round(us[0], 2), "median": round(us[len(us) // 2], 2),
+                "max": round(us[-1], 2), "calls": sum(c for *_, c in pairs),
+                "event_pairs": len(us)}
+
+
+def cpu_cores() -> tuple[int, str]:
+    """Host threads the CPU baseline uses: every core in this process's affinity set, limited by
+    the cgroup CPU quota when one is set (the share a container or job actually gets)."""
+    cores = len(os.sched_getaffinity(0))
+    how = f"{cores} cores in the affinity set"
+    quota = None
+    try:
+        text = Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        if text and text[0] != "max":
+            quota = int(text[0]) / int(text[1])
+    except (OSError, ValueError, IndexError):
+        try:
+            q = int(Path("/sys/fs/cgroup/cpu/cpu.cfs_quota_us").read_text())
+            per = int(Path("/sys/fs/cgroup/cpu/cpu.cfs_period_us").read_text())
+            quota = q / per if q > 0 else None
+        except (OSError, ValueError):
+            quota = None
+    if quota is not None and int(quota) < cores:
+        cores = max(1, int(quota))
+        how += f", cgroup CPU quota {quota:g}"
+    return cores, how
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_time(fn, min_reps: int = 3, max_reps: int = 5, long_s: float = 3.0) -> float:
+    """Median seconds of fn() on the host after one warm-up call: max_reps repetitions, or
+    min_reps when one call takes longer than long_s."""
+    import statistics
+
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    reps = min_reps if first > long_s else max_reps
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def oracle_mx_update_threaded(pool, workers, q, e, m, x, dt, A, B, C, D, dt_bias, bits, seed,
+                              rng_offset):
+    """The CPU oracle's MX update (oracle.mx_state.mx_update, counter rounding) split over batch
+    chunks run on `workers` threads (rows are independent; each chunk's counter offset is its
+    first element's index, so the draws are the same as one call's). numpy and torch release the
+    GIL inside their kernels, so the chunks run in parallel."""
+    from oracle import mx_state as omx
+
+    bsz = q.shape[0]
+    per = q[0].size
+    bounds = [(bsz * i // workers, bsz * (i + 1) // workers) for i in range(workers)]
+    bounds = [(a, b) for a, b in bounds if b > a]
+
+    def one(ab):
+        a, b = ab
+        return omx.mx_update(q[a:b], e[a:b], m[a:b], x[a:b], dt[a:b], A, B[a:b], C[a:b], D=D,
+                             dt_bias=dt_bias, dt_softplus=True, format_bits=bits,
+                             round_mode=omx.ROUND_SR_COUNTER, seed=seed,
+                             rng_offset=rng_offset + a * per)
+
+    return list(pool.map(one, bounds))
 
 
 def _mx_tensors(torch, shape, bits, layout, dev):
@@ -162,12 +264,14 @@ def run_step(torch, args, attn, mamba, ev=None):
     B, S, g = args.batch, args.ctx, args.group
     total_state = B * 128 * 64 * 128
 
-    def call(name, fn):
+    def call(name, fn, calls=1):
         if ev is None:
             fn()
         else:
-            ev.around(name, fn)
+            ev.around(name, fn, calls)
 
+    # attention layers: pack then attend, per layer; each call timed by its own event pair
+    # (about 1 % of event overhead on the 225 us attention call)
     for L in attn:
         call("pack", lambda: _abi.int4_pack_kv_pair(L["k_new"], L["v_new"], L["k_packed"],
                                                     L["v_packed"], L["k_scale"], L["v_scale"],
@@ -175,20 +279,46 @@ def run_step(torch, args, attn, mamba, ev=None):
         call("attention", lambda: _abi.int4_decode_attention(
             L["q"], L["k_packed"], L["v_packed"], L["k_scale"], L["v_scale"], None, L["out"], S,
             4, g))
-    for M in mamba:
-        off = M["step"] * total_state
-        call("mx_update", lambda: _abi.mx_state_update(
-            *M["st"], M["x"], M["dt"], M["dt_bias"], M["A"], M["B"], M["C"], M["D"], None,
-            M["out"], args.state_bits, True, _abi.ROUND_SR_COUNTER, seed=1234, rng_offset=off))
-        M["step"] += 1
+
+    # the Mamba layers' updates run back to back and are timed as one run per step: an event
+    # pair around every 40 us update adds its own dispatch time (per-call events read 1-2.5 us
+    # above the kernel trace's durations), one pair per run of 24 spreads it over 24 calls
+    def updates():
+        for M in mamba:
+            off = M["step"] * total_state
+            _abi.mx_state_update(
+                *M["st"], M["x"], M["dt"], M["dt_bias"], M["A"], M["B"], M["C"], M["D"], None,
+                M["out"], args.state_bits, True, _abi.ROUND_SR_COUNTER, seed=1234,
+                rng_offset=off)
+            M["step"] += 1
+
+    if mamba:
+        call("mx_update", updates, len(mamba))
 
 
-def sweep(torch, dev, which: str = "all", reps: int = 20):
-    """Per-kernel cold-cache timings over the BASELINE configurations."""
+def _ints(text):
+    return None if not text else [int(v) for v in str(text).split(",") if v.strip()]
+
+
+def sweep(torch, dev, args):
+    """Per-kernel cold-cache timings over the BASELINE configurations, each with the CPU oracle
+    timed on the same inputs (attention at batch 1 and 8, every state update) unless
+    --cpu-pairs off."""
+    from concurrent.futures import ThreadPoolExecutor
+
     from layer_quant_amd import _abi
     from layer_quant_amd.traffic import (attention_bytes, mx_update_bytes, prefill_flops,
                                          ssm_update_bytes)
+    from oracle import int4_kv as oik
+    from oracle import mx_state as omx
 
+    which, reps = args.sweep, args.reps
+    keep_b, keep_s = _ints(args.batches), _ints(args.ctxs)
+    lengths = _ints(args.lengths) or [1024, 4096, 16384]
+    pairs = args.cpu_pairs == "on"
+    cores, how = cpu_cores()
+    torch.set_num_threads(cores)
+    pool = ThreadPoolExecutor(max_workers=cores) if pairs else None
     scratch = torch.ones(512 << 20, dtype=torch.uint8, device=dev)
     gen = torch.Generator(device=dev).manual_seed(0)
     cache_bytes = 256 << 20
@@ -216,12 +346,23 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
         log(f"{kernel} {cfg}: {med:.1f} us, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%})")
         return r
 
+    def cpu_pair(r, fn, what):
+        sec = cpu_time(fn)
+        r["cpu_baseline"] = {"us": round(sec * 1e6, 1), "cores": cores, "kind": "port",
+                             "what": what, "cpu_over_gpu": round(sec * 1e6 / r["median_us"], 1)}
+        log(f"  cpu oracle: {sec * 1e3:.1f} ms ({r['cpu_baseline']['cpu_over_gpu']}x the GPU)")
+
+    def want(b, s=None):
+        return (keep_b is None or b in keep_b) and (s is None or keep_s is None or s in keep_s)
+
     rows = []
     hq, hkv, d, g = 32, 8, 128, 32
     shapes = [(B, S, g) for B in (1, 8, 64) for S in (1024, 4096, 16384)]
     shapes.append((8, 2072, 64))  # the shape of the reference's own published figure (A100)
     shapes.append((64, 16384, 64))  # the reference driver's default group (--kv-group-size 64)
     for B, S, gs in (shapes if which in ("all", "attention") else ()):
+        if not want(B, S):
+            continue
         kp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
         vp = torch.randint(0, 256, (B, hkv, S, d // 2), dtype=torch.uint8, device=dev, generator=gen)
         ks = torch.rand(B, hkv, S, d // gs, device=dev, generator=gen) + 0.01
@@ -229,11 +370,19 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
         q = torch.randn(B, hq, 1, d, device=dev, generator=gen).to(torch.bfloat16)
         out = torch.empty(B, hq, d, device=dev, dtype=torch.bfloat16)
         med, mean = timed(lambda: _abi.int4_decode_attention(q, kp, vp, ks, vs, None, out, S, 4, gs))
-        rows.append(row("int4_decode_attention", attention_bytes(B, hq, hkv, d, S, gs), med, mean,
-                        batch=B, ctx=S, group=gs))
+        r = row("int4_decode_attention", attention_bytes(B, hq, hkv, d, S, gs), med, mean,
+                batch=B, ctx=S, group=gs)
+        if pairs and B <= 8:
+            c = [t.cpu() for t in (q, kp, vp, ks, vs)]
+            cpu_pair(r, lambda: oik.decode_attention(*c, S, 4, gs),
+                     "oracle.int4_kv.decode_attention (float64, dequantizes the packed cache as "
+                     "the reference's kernel does) on the same cache and queries")
+        rows.append(r)
         del kp, vp, ks, vs
     nh, p_, n, ng = 128, 64, 128, 8
     for B in ((1, 8, 64) if which in ("all", "state") else ()):
+        if not want(B):
+            continue
         x = torch.randn(B, nh, p_, device=dev, generator=gen).to(torch.bfloat16)
         dt = torch.randn(B, nh, device=dev, generator=gen).to(torch.bfloat16)[:, :, None].expand(B, nh, p_)
         A = (-torch.exp(torch.rand(nh, device=dev, generator=gen) * 2))[:, None, None].expand(nh, p_, n)
@@ -243,6 +392,7 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
         dtb = (torch.randn(nh, device=dev, generator=gen) * 0.1)[:, None].expand(nh, p_)
         out = torch.empty(B, nh, p_, device=dev, dtype=torch.bfloat16)
         h0 = torch.randn(B, nh, p_, n, device=dev, generator=gen) * 0.5
+        host = [t.cpu() for t in (x, dt, A, Bm, Cm, D, dtb)] if pairs else None
         for bits, layout in ((8, "reference"), (4, "reference"), (8, "compact"), (4, "compact")):
             st = _mx_tensors(torch, (B, nh, p_, n), bits, layout, dev)
             _abi.mx_encode(h0, *st, bits, _abi.ROUND_NEAREST_EVEN)
@@ -254,9 +404,24 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
                                      rng_offset=step[0] * B * nh * p_ * n)
                 step[0] += 1
             med, mean = timed(upd)
-            rows.append(row(f"mx{bits}_state_update", mx_update_bytes(
+            r = row(f"mx{bits}_state_update", mx_update_bytes(
                 B, nh, p_, n, ng, format_bits=bits, layout=layout), med, mean, batch=B,
-                layout=layout, rounding="stochastic (counter)"))
+                layout=layout, rounding="stochastic (counter)")
+            if pairs and layout == "reference":
+                qh, eh, mh = (t.cpu().numpy() for t in st)
+                hx, hdt, hA, hB, hC, hD, hdtb = host
+
+                def cpu_upd():
+                    torch.set_num_threads(1)
+                    try:
+                        oracle_mx_update_threaded(pool, cores, qh, eh, mh, hx, hdt, hA, hB, hC,
+                                                  hD, hdtb, bits, 1234, 0)
+                    finally:
+                        torch.set_num_threads(cores)
+                cpu_pair(r, cpu_upd, "oracle.mx_state.mx_update (decode, fp32 update, counter "
+                                     "writeback), batch chunks on every thread, same state and "
+                                     "inputs")
+            rows.append(r)
         # the BASELINE configurations' seeded uniform tensor (reference formula, bit-exact mode):
         # the fp32 tensor adds 4 bytes per state element to the traffic
         uni = torch.rand(B, nh, p_, n, device=dev, generator=gen)
@@ -273,10 +438,19 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
         state = h0.to(torch.bfloat16)
         med, mean = timed(lambda: _abi.selective_state_update(state, x, dt, dtb, A, Bm, Cm, D, None,
                                                               out, True))
-        rows.append(row("bf16_selective_state_update", ssm_update_bytes(B, nh, p_, n, ng), med, mean,
-                        batch=B))
-    for L in ((1024, 4096, 16384) if which in ("all", "prefill") else ()):
-        # causal prefill over the packed cache of one attention layer, batch 1 (MFMA-bound)
+        r = row("bf16_selective_state_update", ssm_update_bytes(B, nh, p_, n, ng), med, mean,
+                batch=B)
+        if pairs:
+            hs = state.cpu()
+            hx, hdt, hA, hB, hC, hD, hdtb = host
+            cpu_pair(r, lambda: omx.bf16_state_update(hs, hx, hdt, hA, hB, hC, D=hD,
+                                                      dt_bias=hdtb, dt_softplus=True),
+                     "oracle.mx_state.bf16_state_update (torch fp32, intra-op threads), same "
+                     "state and inputs")
+        rows.append(r)
+    for L in (lengths if which in ("all", "prefill") else ()):
+        # causal prefill over the packed cache of one attention layer, batch 1 (MFMA-bound); no
+        # CPU pair: the float64 oracle's L x L scores at L = 16384 need 69 GB
         kp = torch.randint(0, 256, (1, hkv, L, d // 2), dtype=torch.uint8, device=dev, generator=gen)
         vp = torch.randint(0, 256, (1, hkv, L, d // 2), dtype=torch.uint8, device=dev, generator=gen)
         ks = torch.rand(1, hkv, L, d // g, device=dev, generator=gen) + 0.01
@@ -293,9 +467,15 @@ def sweep(torch, dev, which: str = "all", reps: int = 20):
         log(f"int4_prefill_attention L={L}: {med:.1f} us, {tfs:.0f} TFLOP/s "
             f"({tfs / PEAK_BF16_TFLOPS:.1%} of bf16 MFMA)")
         del kp, vp, ks, vs, q, out
+    if pool is not None:
+        pool.shutdown()
     return {"sweep": rows, "reps": reps, "timing": "median of per-call HIP events, each call after a "
             "512 MB scratch read (a read evicts the caches without leaving dirty lines whose "
-            "write-back would compete with the timed kernel)", "peak_GB_s": PEAK_HBM_GBS}
+            "write-back would compete with the timed kernel)", "peak_GB_s": PEAK_HBM_GBS,
+            "cpu": {"cores": cores, "how": how, "model": cpu_model(),
+                    "timing": "median of 5 calls after one warm-up (3 when a call takes over 3 s)",
+                    "inputs": "host copies of the GPU row's inputs, already in memory"}
+            if pairs else None}
 
 
 def config1_gpu(torch, dev, reps: int = 20) -> float:
@@ -335,54 +515,56 @@ def config1_gpu(torch, dev, reps: int = 20) -> float:
 
 
 def cpu_baseline(args):
-    """The CPU oracle (torch fp32/fp64 restatement of the reference formulas) on a bounded
-    sample of the same step, on this host's cores, scaled linearly to the full step."""
-    import numpy as np
+    """The CPU oracle (torch/numpy restatement of the reference formulas, tests' checker) timed on
+    this host: one attention layer on a batch sample (pack the new K and V token, attend over the
+    full context), scaled to the full batch, and one MX update at the full batch split over every
+    core; both times the step's layer counts. Inputs are host tensors already in memory."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import torch
 
     from oracle import int4_kv as oik
     from oracle import mx_state as omx
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores, how = cpu_cores()
     torch.set_num_threads(cores)
     gen = torch.Generator().manual_seed(0)
     hq, hkv, d, g = 32, 8, 128, args.group
-    s_sample = args.ctx
-    ba_sample = min(args.batch, 2)
-    cache = oik.allocate_cache(ba_sample, hkv, s_sample, d, g)
-    kv = torch.randn(ba_sample, hkv, s_sample, d, generator=gen).to(torch.bfloat16)
-    oik.pack_kv_into_cache(cache, kv, kv, torch.arange(s_sample), g)
+    S = args.ctx
+    ba = min(args.batch, 2)
+    cache = oik.allocate_cache(ba, hkv, S, d, g)
+    kv = torch.randn(ba, hkv, S, d, generator=gen).to(torch.bfloat16)
+    oik.pack_kv_into_cache(cache, kv, kv, torch.arange(S), g)
     del kv
-    q = torch.randn(ba_sample, hq, 1, d, generator=gen).to(torch.bfloat16)
-    new = torch.randn(ba_sample, hkv, 1, d, generator=gen).to(torch.bfloat16)
+    q = torch.randn(ba, hq, 1, d, generator=gen).to(torch.bfloat16)
+    new = torch.randn(ba, hkv, 1, d, generator=gen).to(torch.bfloat16)
 
     def attn_once():
-        oik.pack_into(cache["k_packed"], cache["k_scale"], new, torch.tensor([s_sample - 1]), g)
-        oik.pack_into(cache["v_packed"], cache["v_scale"], new, torch.tensor([s_sample - 1]), g)
+        oik.pack_into(cache["k_packed"], cache["k_scale"], new, torch.tensor([S - 1]), g)
+        oik.pack_into(cache["v_packed"], cache["v_scale"], new, torch.tensor([S - 1]), g)
         oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
-                             cache["v_scale"], s_sample, 4, g)
+                             cache["v_scale"], S, 4, g)
 
-    b_sample = min(args.batch, 8)
-    shape = (b_sample, 128, 64, 128)
-    qs, es, ms_ = omx.mx_encode((torch.randn(shape, generator=gen) * 0.5).numpy(), args.state_bits)
-    x = torch.randn(b_sample, 128, 64, generator=gen).to(torch.bfloat16)
-    dt = torch.randn(b_sample, 128, 64, generator=gen).to(torch.bfloat16)
-    A = -torch.rand(128, generator=gen)[:, None, None].expand(128, 64, 128)
-    Bm = torch.randn(b_sample, 8, 128, generator=gen).to(torch.bfloat16)
-    D = torch.randn(128, generator=gen)[:, None].expand(128, 64)
+    bm = args.batch
+    nh, p_, n, ng = 128, 64, 128, 8
+    qs, es, ms_ = omx.mx_encode((torch.randn(bm, nh, p_, n, generator=gen) * 0.5).numpy(),
+                                args.state_bits)
+    x = torch.randn(bm, nh, p_, generator=gen).to(torch.bfloat16)
+    dt = torch.randn(bm, nh, 1, generator=gen).to(torch.bfloat16).expand(bm, nh, p_)
+    A = (-torch.exp(torch.rand(nh, generator=gen) * 2))[:, None, None].expand(nh, p_, n)
+    Bm = torch.randn(bm, ng, n, generator=gen).to(torch.bfloat16)
+    Cm = torch.randn(bm, ng, n, generator=gen).to(torch.bfloat16)
+    D = torch.randn(nh, generator=gen)[:, None].expand(nh, p_)
+    dtb = (torch.randn(nh, generator=gen) * 0.1)[:, None].expand(nh, p_)
+    pool = ThreadPoolExecutor(max_workers=cores)
 
     def mx_once():
-        omx.mx_update(qs, es, ms_, x, dt, A, Bm, Bm, D=D, dt_bias=D * 0.1, dt_softplus=True,
-                      format_bits=args.state_bits, round_mode=omx.ROUND_SR_COUNTER, seed=1234)
-
-    def timed(fn, reps):
-        fn()
-        ts = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t0)
-        return float(np.median(ts))
+        torch.set_num_threads(1)  # one thread per chunk; the pool supplies the parallelism
+        try:
+            oracle_mx_update_threaded(pool, cores, qs, es, ms_, x, dt, A, Bm, Cm, D, dtb,
+                                      args.state_bits, 1234, 0)
+        finally:
+            torch.set_num_threads(cores)
 
     # BASELINE config 1 (the reference's CPU-runnable case): pack a 1024-token K/V cache and
     # attend once, batch 1, 32 q / 8 KV heads, group 32, seed 0
@@ -396,25 +578,27 @@ def cpu_baseline(args):
         oik.decode_attention(q1, c1["k_packed"], c1["v_packed"], c1["k_scale"], c1["v_scale"],
                              1024, 4, g1)
 
-    reps = 3
-    t_cfg1 = timed(config1_once, 5)
-    t_attn = timed(attn_once, reps)
-    t_mx = timed(mx_once, reps)
-    scale_attn = (args.batch / ba_sample) * (args.ctx / s_sample)
-    scale_mx = args.batch / b_sample
-    step_s = args.attn_layers * t_attn * scale_attn + args.mamba_layers * t_mx * scale_mx
+    t_cfg1 = cpu_time(config1_once)
+    t_attn = cpu_time(attn_once)
+    t_mx = cpu_time(mx_once)
+    pool.shutdown()
+    scale_attn = args.batch / ba
+    step_s = args.attn_layers * t_attn * scale_attn + args.mamba_layers * t_mx
     return {
         "value": round(step_s * 1e6, 1),
         "unit": "us/step",
         "cores": cores,
         "kind": "port",
-        "sample": (f"oracle (torch/numpy CPU, torch threads = cores; numpy elementwise work "
-                   f"single-threaded) on 1 attention layer at batch {ba_sample}, ctx {s_sample} "
-                   f"(pack K,V + attend) and 1 MX{args.state_bits} update at batch {b_sample}, "
-                   f"median of {reps} after one warm-up, scaled linearly to {args.attn_layers} "
-                   f"layers x batch {args.batch} x ctx {args.ctx} and {args.mamba_layers} layers x "
-                   f"batch {args.batch}; attention {t_attn * 1e3:.1f} ms, update "
-                   f"{t_mx * 1e3:.1f} ms per sample call"),
+        "sample": (f"oracle (torch/numpy CPU) on {cores} threads ({how}; {cpu_model()}): one "
+                   f"attention layer at batch {ba}, ctx {S} (pack the new K and V token + "
+                   f"attend, torch intra-op threads) {t_attn * 1e3:.1f} ms, scaled x{scale_attn:g} "
+                   f"to batch {args.batch}; one MX{args.state_bits} update at the full batch "
+                   f"{args.batch} (timed directly, batch chunks on {cores} threads) "
+                   f"{t_mx * 1e3:.1f} ms; medians after one warm-up; step = "
+                   f"{args.attn_layers} x attention + {args.mamba_layers} x update"),
+        "legs_ms": {"attention_layer_sample": round(t_attn * 1e3, 2),
+                    "attention_layer_scale": scale_attn,
+                    "mx_update_full_batch": round(t_mx * 1e3, 2)},
         "config1_us": round(t_cfg1 * 1e6, 1),
     }
 
@@ -446,7 +630,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     if args.sweep:
-        print(json.dumps(sweep(torch, dev, args.sweep)), flush=True)
+        print(json.dumps(sweep(torch, dev, args)), flush=True)
         return
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
@@ -462,6 +646,18 @@ def main():
     for _ in range(args.warmup):
         run_step(torch, args, attn, mamba)
     torch.cuda.synchronize()
+    # settle: untimed steps until the clocks have ramped up (in kernel traces of this workload
+    # the MX update took ~50 us in the first steps and ~40 us from about the 25th on, while the
+    # HBM-bound attention stayed flat)
+    settle_steps = 0
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < args.settle_seconds:
+        for _ in range(5):
+            run_step(torch, args, attn, mamba)
+            settle_steps += 1
+        torch.cuda.synchronize()
+    settle_s = time.perf_counter() - t_settle
+    log(f"settle: {settle_steps} steps in {settle_s:.3f} s")
 
     # timed region 1: whole steps, no per-kernel events
     t0 = time.perf_counter()
@@ -471,7 +667,7 @@ def main():
     step_s = (time.perf_counter() - t0) / args.steps
     log(f"step: {step_s * 1e6:.1f} us")
 
-    # timed region 2: the same steps with HIP events around every kernel call
+    # timed region 2: the same steps with HIP events around the kernel calls (see run_step)
     ev = Events(torch)
     for _ in range(args.steps):
         run_step(torch, args, attn, mamba, ev)
@@ -486,7 +682,8 @@ def main():
                          "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
                          "calls_per_step": {"attention": args.attn_layers,
                                             "pack": args.attn_layers,
-                                            "mx_update": args.mamba_layers}[name]}
+                                            "mx_update": args.mamba_layers}[name],
+                         "per_call_us": ev.spread_us(name)}
         log(f"{name}: {us:.1f} us/call, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%})")
     dominant = max(kernels, key=lambda k: kernels[k]["us"] * kernels[k]["calls_per_step"])
     dk = kernels[dominant]
@@ -503,6 +700,12 @@ def main():
         "unit": "GB/s",
         "frac": dk["frac_of_peak"],
         "traffic": load_traffic(dominant, workload),
+        "timing": (f"HIP events on the launch stream over the {args.steps} timed steps, "
+                   + ("one pair around each call" if dominant != "mx_update" else
+                      f"one pair around each step's {args.mamba_layers} back-to-back updates")
+                   + f" ({dk['per_call_us']['calls']} calls; per-pair mean per call min / "
+                   f"median / max {dk['per_call_us']['min']} / {dk['per_call_us']['median']} / "
+                   f"{dk['per_call_us']['max']} us)"),
     }
     cfg1_gpu = config1_gpu(torch, dev)
     cpu = None
@@ -522,6 +725,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"steps": settle_steps, "seconds": round(settle_s, 3),
+                   "note": "untimed steps after the warmup until the GPU clocks settle"},
         "ms_per_step": round(step_s * 1e3, 4),
         "higher_is_better": False,
         "scaling": "weak",
