@@ -1,7 +1,8 @@
 // MFMA fast path of the INT4 decode attention (head_dim 128, group 32/64/128, bf16 queries).
 //
-// One workgroup = 4 waves on one (batch, KV head, key split); each wave walks its own key range
-// in tiles of 32 keys and the 4 partial softmax states are merged through LDS at the end.
+// One workgroup = 4 waves on one (batch, KV head, key split); the split's 32-key tiles are dealt
+// to the waves in turn (wave w takes tiles w, w + 4, ...) and the 4 partial softmax states are
+// merged through LDS at the end.
 // Every packed KV byte and scale is read from HBM once per (batch, KV head): the NREP query
 // heads that share a KV head are columns of the same MFMA tile.
 //
@@ -259,9 +260,13 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   const int S = (int)p.S;
   const int t0 = split * (int)p.chunk;
   const int t1 = min(S, t0 + (int)p.chunk);
-  const int tpw = (int)p.chunk / WAVES;
-  const int w0 = t0 + wave * tpw;
-  const int w1 = min(t1, w0 + tpw);
+  // The workgroup's tiles are dealt to its waves in turn (wave w takes tiles w, w + 4, ...): the
+  // four waves then read adjacent tiles, one stream per tensor per workgroup. With a contiguous
+  // range per wave (four streams per tensor per workgroup) a read-only probe of this pattern ran
+  // at 6.55 TB/s against 6.99 TB/s interleaved.
+  const int ntile = (t1 - t0 + TILE - 1) / TILE;
+  const int nw = ntile > wave ? (ntile - wave + WAVES - 1) / WAVES : 0;  // tiles of this wave
+  auto tile_key = [&](const int i) { return t0 + (wave + WAVES * i) * TILE; };
 
   const bool colvalid = c16 < NCOL;
   const int colh = c16 % NREP;
@@ -279,8 +284,8 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   R.mask_len = p.mask_len;
 
   // the first tiles' loads go out before the query set-up
-  if (w0 < w1) issue_tile<G, MASK>(R, w0, S, tiles0[wave], lane);
-  if (w0 + TILE < w1) issue_tile<G, MASK>(R, w0 + TILE, S, tiles1[wave], lane);
+  if (nw > 0) issue_tile<G, MASK>(R, tile_key(0), S, tiles0[wave], lane);
+  if (nw > 1) issue_tile<G, MASK>(R, tile_key(1), S, tiles1[wave], lane);
 
   // Query operands. Lane (q, .) feeds MFMA c with dword c of its key unit q, i.e. dims
   // 32q + 8c .. 32q + 8c + 7 (slot order kPerm); the query is placed only in the columns whose
@@ -323,16 +328,17 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   f32x4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
   const u32x4_t ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
 
-  // Before tile tb's reads: wait for its loads, leaving the already issued loads of the
-  // following tiles (LPT each) in flight.
-  auto wait_tile = [&](const int tb) {
-    if (tb + 2 * TILE < w1) wait_loads<2 * LPT>();
-    else if (tb + TILE < w1) wait_loads<LPT>();
+  // Before the reads of the wave's tile i: wait for its loads, leaving the already issued loads
+  // of its following tiles (LPT each) in flight.
+  auto wait_tile = [&](const int i) {
+    if (i + 2 < nw) wait_loads<2 * LPT>();
+    else if (i + 1 < nw) wait_loads<LPT>();
     else wait_loads<0>();
   };
 
-  auto process = [&](const int tb, const TileLds& B) {
-    wait_tile(tb);
+  auto process = [&](const int i, const TileLds& B) {
+    const int tb = tile_key(i);
+    wait_tile(i);
     // scores S^T (keys x columns) in raw units: two 16-key halves, 4 chunks each
     f32x4_t sacc[2];
     sacc[0] = f32x4_t{cinit, cinit, cinit, cinit};
@@ -402,12 +408,12 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
         }
       }
     }
-    if (tb + TILE > w1) {  // keys past this wave's range: no score, no value scale
+    if (tb + TILE > t1) {  // keys past this workgroup's range: no score, no value scale
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int tok = tb + 16 * (e >> 2) + 4 * (e & 3) + q4;
-        s[e] = tok < w1 ? s[e] : -INFINITY;
-        vsc[e] = tok < w1 ? vsc[e] : 0.0f;
+        s[e] = tok < t1 ? s[e] : -INFINITY;
+        vsc[e] = tok < t1 ? vsc[e] : 0.0f;
       }
     }
     // Lazy rescaling: p = 2^(csm s - m_run) with a running max that only moves when a score
@@ -473,15 +479,15 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   // 3-deep ring of LDS tiles: the loads of the next 2 tiles are in flight while one is processed
   // (unrolled by 3 so that each ring position is its own LDS object; a 4th buffer, the whole
   // 160 KB of LDS per CU at 2 workgroups, measured no faster)
-  for (int tb = w0; tb < w1; tb += 3 * TILE) {
-    if (tb + 2 * TILE < w1) issue_tile<G, MASK>(R, tb + 2 * TILE, S, tiles2[wave], lane);
-    process(tb, tiles0[wave]);
-    if (tb + TILE >= w1) break;
-    if (tb + 3 * TILE < w1) issue_tile<G, MASK>(R, tb + 3 * TILE, S, tiles0[wave], lane);
-    process(tb + TILE, tiles1[wave]);
-    if (tb + 2 * TILE >= w1) break;
-    if (tb + 4 * TILE < w1) issue_tile<G, MASK>(R, tb + 4 * TILE, S, tiles1[wave], lane);
-    process(tb + 2 * TILE, tiles2[wave]);
+  for (int i = 0; i < nw; i += 3) {
+    if (i + 2 < nw) issue_tile<G, MASK>(R, tile_key(i + 2), S, tiles2[wave], lane);
+    process(i, tiles0[wave]);
+    if (i + 1 >= nw) break;
+    if (i + 3 < nw) issue_tile<G, MASK>(R, tile_key(i + 3), S, tiles0[wave], lane);
+    process(i + 1, tiles1[wave]);
+    if (i + 2 >= nw) break;
+    if (i + 4 < nw) issue_tile<G, MASK>(R, tile_key(i + 4), S, tiles1[wave], lane);
+    process(i + 2, tiles2[wave]);
   }
 
   // per-wave partial -> LDS (in the wave's first tile buffer, whose last reads are complete)
@@ -607,9 +613,10 @@ static int64_t resident_fast_waves() {
 }
 
 SplitPlan plan_fast(int64_t B, int64_t Hkv, int64_t S) {
-  // One resident generation of waves: each wave walks as many keys as that takes (rounded to the
-  // 32-key tile, 4 waves per workgroup split). Fewer, longer waves amortize the per-wave setup
-  // and the 4-wave merge, and at B * Hkv >= resident / 4 no split-K merge runs at all.
+  // One resident generation of waves: each wave gets as many keys as that takes (rounded to the
+  // 32-key tile, 4 waves per workgroup split, the split's tiles dealt to the waves in turn).
+  // Fewer, longer waves amortize the per-wave setup and the 4-wave merge, and at
+  // B * Hkv >= resident / 4 no split-K merge runs at all.
   const int64_t target_waves = resident_fast_waves();
   int64_t tpw = (B * Hkv * S + target_waves - 1) / target_waves;
   tpw = ((tpw + TILE - 1) / TILE) * TILE;

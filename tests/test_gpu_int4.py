@@ -198,9 +198,10 @@ def test_attention_bf16_output(gpu):
 
 @pytest.mark.parametrize("s,g", [(999, 32), (1057, 64), (1150, 128)])
 def test_attention_long_wave_ranges_ragged_tail(gpu, s, g):
-    """B * Hkv = 512: each wave of the MFMA path walks 8-9 tiles of 32 keys through its 3-buffer
-    LDS ring, and the last wave's ragged tile lands on ring position 1, 0 and 2 for the three
-    contexts (one resident generation of 2048 waves, 4 waves per (batch, KV head))."""
+    """B * Hkv = 512: each (batch, KV head) workgroup deals 32-32-36 tiles of 32 keys to its 4
+    waves in turn (8-9 per wave through the 3-buffer LDS ring); the ragged last tile of the range
+    falls to a different wave and ring position for each context (one resident generation of
+    2048 waves)."""
     b, hkv, nrep, d = 64, 8, 4, 128
     cache = _packed_cache(b, hkv, s, d, g, 1200 + s, cap=s + 5)
     q = _activations((b, hkv * nrep, 1, d), 1300 + s, torch.bfloat16)
