@@ -196,12 +196,12 @@ def test_attention_bf16_output(gpu):
     assert_close_rel(out.float(), ref, rtol=8e-3, what="bf16 out")
 
 
-@pytest.mark.parametrize("s,g", [(999, 32), (1057, 64), (1150, 128)])
+@pytest.mark.parametrize("s,g", [(999, 32), (1057, 64), (805, 128)])
 def test_attention_long_wave_ranges_ragged_tail(gpu, s, g):
-    """B * Hkv = 512: each (batch, KV head) workgroup deals 32-32-36 tiles of 32 keys to its 4
-    waves in turn (8-9 per wave through the 3-buffer LDS ring); the ragged last tile of the range
-    falls to a different wave and ring position for each context (one resident generation of
-    2048 waves)."""
+    """B * Hkv = 512 (one resident generation of 2048 waves, one split): each (batch, KV head)
+    workgroup deals its 32, 34 or 26 tiles of 32 keys to its 4 waves in turn, 7-9 per wave through
+    the 3-buffer LDS ring; the ragged last tile (S % 32 = 7, 1, 5) is the wave's tile 7, 8 or 6,
+    i.e. ring position 1, 2 or 0."""
     b, hkv, nrep, d = 64, 8, 4, 128
     cache = _packed_cache(b, hkv, s, d, g, 1200 + s, cap=s + 5)
     q = _activations((b, hkv * nrep, 1, d), 1300 + s, torch.bfloat16)
@@ -211,11 +211,11 @@ def test_attention_long_wave_ranges_ragged_tail(gpu, s, g):
 
 
 def _long_range_masks(b, s):
-    """Masks for B=64 at S ~ 1000, where each wave of the MFMA path walks 256 keys (8 tiles):
-    a keep-mask whose left padding covers a whole wave's range and part of the next (rows 0-7:
-    300-307 keys), padding inside one tile and a gap across a tile edge in other rows; a 4-D
-    additive bias; and a short bias mask that ends inside the third wave's range and inside a
-    tile (700 keys)."""
+    """Masks for B=64 at S ~ 800-1060, where each wave of the MFMA path takes every fourth 32-key
+    tile of its (batch, KV head): a keep-mask whose left padding covers the first 9-10 tiles,
+    i.e. two or more of every wave's tiles (rows 0-7: 300-307 keys), padding inside one tile and
+    a gap across a tile edge in other rows; a 4-D additive bias; and a short bias mask that ends
+    inside a tile (700 keys), so that later tiles of every wave are fully masked."""
     gen = torch.Generator().manual_seed(s)
     keep = torch.ones(b, s, dtype=torch.bool)
     for r in range(8):
@@ -230,7 +230,7 @@ def _long_range_masks(b, s):
     }
 
 
-@pytest.mark.parametrize("s,g", [(999, 32), (1057, 64), (1150, 128)])
+@pytest.mark.parametrize("s,g", [(999, 32), (1057, 64), (805, 128)])
 def test_attention_long_wave_ranges_masked(gpu, s, g):
     """The masked MFMA instance (7 LDS-direct loads per tile) through the whole 3-buffer ring and
     the ragged last tile of each ring position, with masks that end or open inside a wave."""
