@@ -1052,37 +1052,37 @@ static void dispatch_encode(const MxCodecParams& p, int rmode, bool vec, dim3 gr
 }
 
 // Rows kernel geometry: R rows per lane, THREADS threads, one (batch, head) slice of up to
-// R * THREADS / (N/16) rows per workgroup (64 rows = one Nemotron-H head at N = 128).
-#ifndef LQ_MX_ROWS_R
-#define LQ_MX_ROWS_R 2
-#endif
-#ifndef LQ_MX_ROWS_THREADS
-#define LQ_MX_ROWS_THREADS 256
-#endif
-constexpr int ROWS_R = LQ_MX_ROWS_R;
-constexpr int ROWS_THREADS = LQ_MX_ROWS_THREADS;
+// R * THREADS / (N/16) rows per workgroup (64 rows = one Nemotron-H head at N = 128). The reference
+// layout keeps 2 rows per lane (78 VGPRs, 6 waves per SIMD: its 212 MB per call at batch 64 need
+// the waves to hide memory latency; 4 rows per lane take 100 VGPRs, 4 waves, and ran 42.2 against
+// 41.4 us). The compact layouts move 2.5x fewer bytes and are bound by their arithmetic, so 4 rows
+// per lane share the per-lane setup (head scalars, B and C) over twice the rows: 41.1 -> 38.9 us
+// for MX4 at batch 64 (91 VGPRs, 5 waves per SIMD). The supplied-uniform mode keeps 2 rows per
+// lane everywhere: its 16 uniforms per row would take 155-161 VGPRs at 4 rows.
+template <int LY, int RMODE>
+struct RowsGeometry {
+  static constexpr bool wide = LY != LAYOUT_REF && RMODE != LQ_ROUND_SR_UNIFORM;
+  static constexpr int R = wide ? 4 : 2;
+  static constexpr int THREADS = wide ? 128 : 256;
+  static_assert(R * THREADS == 512, "rows_per_workgroup assumes R * THREADS = 512");
+};
+// Rows per workgroup: the same for every layout and mode (R * THREADS = 512 lanes' rows).
+constexpr int rows_per_workgroup(int vbpr_log2) { return 512 >> vbpr_log2; }
+
+template <int FB, int RMODE, int BPR_LOG2, int LY>
+static void launch_rows_mode(const MxUpdateParams& p, dim3 grid, hipStream_t st) {
+  using G = RowsGeometry<LY, RMODE>;
+  hipLaunchKernelGGL((mx_update_rows_kernel<FB, RMODE, BPR_LOG2, G::R, G::THREADS, LY>), grid,
+                     dim3(G::THREADS), 0, st, p);
+}
 
 template <int FB, int BPR_LOG2, int LY>
 static void launch_rows(const MxUpdateParams& p, int rmode, dim3 grid, hipStream_t st) {
-  constexpr int R = ROWS_R, T = ROWS_THREADS;
-  const dim3 block(T);
   switch (rmode) {
-    case LQ_ROUND_NEAREST_EVEN:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_NEAREST_EVEN, BPR_LOG2, R, T, LY>),
-                         grid, block, 0, st, p);
-      break;
-    case LQ_ROUND_HALF_UP:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_HALF_UP, BPR_LOG2, R, T, LY>), grid,
-                         block, 0, st, p);
-      break;
-    case LQ_ROUND_SR_UNIFORM:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_UNIFORM, BPR_LOG2, R, T, LY>),
-                         grid, block, 0, st, p);
-      break;
-    default:
-      hipLaunchKernelGGL((mx_update_rows_kernel<FB, LQ_ROUND_SR_COUNTER, BPR_LOG2, R, T, LY>),
-                         grid, block, 0, st, p);
-      break;
+    case LQ_ROUND_NEAREST_EVEN: launch_rows_mode<FB, LQ_ROUND_NEAREST_EVEN, BPR_LOG2, LY>(p, grid, st); break;
+    case LQ_ROUND_HALF_UP: launch_rows_mode<FB, LQ_ROUND_HALF_UP, BPR_LOG2, LY>(p, grid, st); break;
+    case LQ_ROUND_SR_UNIFORM: launch_rows_mode<FB, LQ_ROUND_SR_UNIFORM, BPR_LOG2, LY>(p, grid, st); break;
+    default: launch_rows_mode<FB, LQ_ROUND_SR_COUNTER, BPR_LOG2, LY>(p, grid, st); break;
   }
 }
 
@@ -1273,7 +1273,7 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
     const View dt0{p.dt.data, p.dt.dtype, {0, 0, 0, 0}};
     if (!p.has_dtb) p.dtb = dt0;
     if (!p.has_D) p.D = dt0;
-    const int rows = ROWS_R * (ROWS_THREADS >> p.vbpr_log2);
+    const int rows = rows_per_workgroup(p.vbpr_log2);
     const dim3 rgrid((unsigned)((P + rows - 1) / rows), (unsigned)H, (unsigned)Bn);
     if (format_bits == 8) {
       rc = with_layout<8>(layout, [&](auto ly) { dispatch_rows<8, ly()>(p, round_mode, rgrid, s); });
