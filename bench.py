@@ -57,6 +57,9 @@ def parse_args():
                          "first ~50 ms, and the VALU-heavy MX update runs 20-25 %% slower "
                          "before they settle")
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    ap.add_argument("--layout-pair", choices=["on", "off"], default="on",
+                    help="after the timed steps, time the same MX updates on compact-layout "
+                         "states (layout_pair in the line; reference-layout runs only)")
     ap.add_argument("--sweep", nargs="?", const="all", default=None,
                     choices=["all", "attention", "state", "prefill"],
                     help="instead of the decode step, time each kernel alone over the BASELINE "
@@ -617,6 +620,41 @@ def load_traffic(kernel: str, workload: str):
     return entry.get("bytes_per_launch")
 
 
+def layout_pair(torch, args, dev, mamba, ref_us):
+    """The step's MX updates on compact-layout states: the same inputs, layer count, rounding
+    and timing (one event pair around each step's run of back-to-back updates) as the timed
+    region, with fresh states encoded from h0 ~ N(0, 0.5)."""
+    from layer_quant_amd import _abi
+    from layer_quant_amd.traffic import mx_update_bytes
+
+    B, nh, p_, n, ng = args.batch, 128, 64, 128, 8
+    gen = torch.Generator(device=dev).manual_seed(1)
+    layers = []
+    for M in mamba:
+        h0 = torch.randn(B, nh, p_, n, device=dev, generator=gen) * 0.5
+        st = _mx_tensors(torch, (B, nh, p_, n), args.state_bits, "compact", dev)
+        _abi.mx_encode(h0, *st, args.state_bits, _abi.ROUND_NEAREST_EVEN)
+        del h0
+        layers.append(dict(M, st=st, step=0))
+    for _ in range(3):
+        run_step(torch, args, [], layers)
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    for _ in range(args.steps):
+        run_step(torch, args, [], layers, ev)
+    torch.cuda.synchronize()
+    us = ev.mean_us("mx_update")
+    nbytes = mx_update_bytes(B, nh, p_, n, ng, format_bits=args.state_bits, layout="compact")
+    del layers
+    return {"what": (f"the step's {len(mamba)} MX{args.state_bits} updates on compact-layout "
+                     "states (nibble mantissas, bit micro-exponents; same values), timed as the "
+                     "reference-layout updates of the line"),
+            "reference_us": round(ref_us, 2), "compact_us": round(us, 2),
+            "compact_algorithmic_bytes": nbytes,
+            "compact_GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "compact_over_reference_time": round(us / ref_us, 4)}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -707,6 +745,11 @@ def main():
                    f"median / max {dk['per_call_us']['min']} / {dk['per_call_us']['median']} / "
                    f"{dk['per_call_us']['max']} us)"),
     }
+    pair = None
+    if args.layout_pair == "on" and args.state_layout == "reference" and mamba:
+        log("compact-layout MX updates")
+        pair = layout_pair(torch, args, dev, mamba, kernels["mx_update"]["us"])
+        log(f"compact layout: {pair['compact_us']} us/call against {pair['reference_us']} us")
     cfg1_gpu = config1_gpu(torch, dev)
     cpu = None
     cfg1 = None
@@ -750,6 +793,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "config1_cpu_vs_gpu": cfg1,
+        "layout_pair": pair,
     }
     print(json.dumps(line), flush=True)
 
