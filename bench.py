@@ -274,7 +274,7 @@ def run_step(torch, args, attn, mamba, ev=None):
             ev.around(name, fn, calls)
 
     # attention layers: pack then attend, per layer; each call timed by its own event pair
-    # (about 1 % of event overhead on the 225 us attention call)
+    # (1-3 % of event overhead on the 215 us attention call)
     for L in attn:
         call("pack", lambda: _abi.int4_pack_kv_pair(L["k_new"], L["v_new"], L["k_packed"],
                                                     L["v_packed"], L["k_scale"], L["v_scale"],
