@@ -664,17 +664,42 @@ __device__ __forceinline__ void load_rows(const MxUpdateParams& p, const HeadBuf
   }
 }
 
-// Update, y, and writeback encode of the R rows held in L.
-template <int FB, int RMODE, int BPR_LOG2, int R, int SLOTS, int LY>
+// Update, y, and writeback encode of the R rows held in L. bdp and cvp point to the lane's 16
+// values of B * dt and C in LDS. With BC_REREAD they are read again for every row instead of
+// once into 32 VGPRs: the compact layouts' 4-row form then fits 74 VGPRs (6 waves per SIMD
+// instead of 5; MX4 at batch 64 38.7 -> 37.1 us, batch 128 72.0 -> 68.1 us on one box), while
+// the reference layout's 2-row form keeps the register copy (7 waves per SIMD without it ran
+// 42.5 against 39.6 us).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int FB, int RMODE, int BPR_LOG2, int R, int SLOTS, int LY, bool BC_REREAD>
 __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadBufs& hb, int b,
                                             int h, int row0, int slot, int blk,
-                                            const RowLoads<R>& L, const float (&Bd)[16],
-                                            const float (&Cv)[16], const HeadScalars& hs) {
+                                            const RowLoads<R>& L, const float* bdp,
+                                            const float* cvp, const HeadScalars& hs) {
   constexpr uint32_t N = 16u << BPR_LOG2;
   const uint32_t n0 = (uint32_t)blk * 16u;
   const int P = p.P;
+  float Bd[16], Cv[16];
+  auto read_bc = [&] {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4_t bq = *(const f32x4_t*)&bdp[4 * i];
+      const f32x4_t cq = *(const f32x4_t*)&cvp[4 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        Bd[4 * i + j] = bq[j];
+        Cv[4 * i + j] = cq[j];
+      }
+    }
+  };
+  if constexpr (!BC_REREAD) read_bc();
 #pragma unroll
   for (int r = 0; r < R; ++r) {
+    if constexpr (BC_REREAD) {
+      asm volatile("" ::: "memory");  // keeps the compiler from reusing the previous row's copy
+      read_bc();
+    }
     const int pp = row0 + r * SLOTS + slot;
     const bool act = pp < P;
     const uint32_t pc = (uint32_t)min(pp, P - 1);
@@ -758,8 +783,6 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
   }
 }
 
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
 // One work item per workgroup: grid (ceil(P / (R * SLOTS)), H, B). Every state load of the lane
 // (R state blocks, x, z) is issued before the first use of any of them; B, C and the head scalars
 // come through LDS (one barrier).
@@ -807,22 +830,12 @@ void mx_update_rows_kernel(MxUpdateParams p) {
     }
   }
   __syncthreads();
-  float Bd[16], Cv[16];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f32x4_t bq = *(const f32x4_t*)&s_bd[n0 + 4 * i];
-    const f32x4_t cq = *(const f32x4_t*)&s_c[n0 + 4 * i];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      Bd[4 * i + j] = bq[j];
-      Cv[4 * i + j] = cq[j];
-    }
-  }
   HeadScalars hs;
-  hs.dt = 0.0f;  // folded into Bd
+  hs.dt = 0.0f;  // folded into B * dt
   hs.dA = s_hs[0];
   hs.D = s_hs[1];
-  update_rows<FB, RMODE, BPR_LOG2, R, SLOTS, LY>(p, hb, b, h, row0, slot, blk, L, Bd, Cv, hs);
+  update_rows<FB, RMODE, BPR_LOG2, R, SLOTS, LY, (LY != LAYOUT_REF)>(p, hb, b, h, row0, slot, blk, L,
+                                                              &s_bd[n0], &s_c[n0], hs);
 }
 
 template <int FB, int RMODE, bool VEC, int LY>
