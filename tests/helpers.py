@@ -10,6 +10,19 @@ RTOL = 2e-3  # the attention output / updated state tolerance, fp32 accumulation
 REPORT: list[str] = []
 
 
+def to_device(t: torch.Tensor | None, device) -> torch.Tensor | None:
+    """t on `device` with its broadcast (stride-0) dimensions kept. Tensor.to copies an expanded
+    tensor into a contiguous one, which would hand the library another layout than the model's
+    (dt, A, D and dt_bias expanded along head_dim select the state updates' row kernels)."""
+    if t is None:
+        return None
+    bcast = [s == 0 and n > 1 for s, n in zip(t.stride(), t.shape)]
+    if not any(bcast):
+        return t.to(device)
+    base = t[tuple(slice(0, 1) if b else slice(None) for b in bcast)]
+    return base.to(device).expand(t.shape)
+
+
 def assert_close_rel(out: torch.Tensor, ref: torch.Tensor, rtol: float = RTOL, what: str = ""):
     """|out - ref| <= rtol * (|ref| + mean|ref|) elementwise, and the relative Frobenius error
     <= rtol. The mean|ref| term keeps outputs that cancel to nearly zero from demanding a

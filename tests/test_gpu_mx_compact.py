@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 import torch
 
+from helpers import to_device
 from hybrid_quant import mamba_state_8b_kernel as ms
 from layer_quant_amd import _abi
 from oracle import mx_state as omx
@@ -41,8 +42,12 @@ def _as_np(t):
 
 @pytest.fixture(params=["rows", "general"])
 def path(request, monkeypatch):
+    """The row kernel (required: the library refuses a call that would take the general
+    kernel), then the general kernel forced."""
     if request.param == "general":
         monkeypatch.setenv("LQ_MX_FORCE_GENERIC", "1")
+    else:
+        monkeypatch.setenv("LQ_MX_REQUIRE_ROWS", "1")
     return request.param
 
 
@@ -87,7 +92,7 @@ def test_update_compact_equals_reference_layout(gpu, path, fb, mode, n):
     bsz, nh, p_, ng = 3, 16, 64, 4
     shape = (bsz, nh, p_, n)
     h0 = _state(shape, 20 + n)
-    t = {k: v.to(gpu) for k, v in _inputs(bsz, nh, p_, n, ng, 21 + fb).items()}
+    t = {k: to_device(v, gpu) for k, v in _inputs(bsz, nh, p_, n, ng, 21 + fb).items()}
     uni = torch.rand(shape, generator=torch.Generator().manual_seed(22)).to(gpu)
     states, ys = {}, {}
     for layout in ("reference", "compact"):
@@ -119,7 +124,7 @@ def test_module_api_compact_chain_and_conversion(gpu, fb):
     for a, b_ in ((conv.q_state, cmp_.q_state), (conv.shared_exp, cmp_.shared_exp),
                   (conv.micro_exp, cmp_.micro_exp)):
         assert torch.equal(a.view(torch.uint8), b_.view(torch.uint8))
-    t = {k: v.to(gpu) for k, v in _inputs(bsz, nh, p_, n, ng, 31).items()}
+    t = {k: to_device(v, gpu) for k, v in _inputs(bsz, nh, p_, n, ng, 31).items()}
     for _ in range(4):
         y1 = ms.mx_state_selective_update(ref, **t, dt_softplus=True)
         y2 = ms.mx_state_selective_update(cmp_, **t, dt_softplus=True)
@@ -133,13 +138,14 @@ def test_module_api_compact_chain_and_conversion(gpu, fb):
     assert torch.equal(ms.dequantize_state_cache(cmp_), ms.dequantize_state_cache(ref))
 
 
-def test_full_size_b64_compact_mx4(gpu):
+def test_full_size_b64_compact_mx4(gpu, monkeypatch):
     """Nemotron-H layer at batch 64 in the compact MX4 layout (row kernel), one counter-mode
     step: bit-identical to the reference layout."""
+    monkeypatch.setenv("LQ_MX_REQUIRE_ROWS", "1")
     bsz, nh, p_, n, ng = 64, 128, 64, 128, 8
     g = torch.Generator(device=gpu).manual_seed(8)
     h0 = torch.randn(bsz, nh, p_, n, device=gpu, generator=g) * 0.5
-    t = {k: v.to(gpu) for k, v in _inputs(bsz, nh, p_, n, ng, 9).items()}
+    t = {k: to_device(v, gpu) for k, v in _inputs(bsz, nh, p_, n, ng, 9).items()}
     out = {}
     for layout in ("reference", "compact"):
         c = ms.allocate_state_kernel_cache(h0, format_bits=4, layout=layout)

@@ -14,7 +14,7 @@ import random
 import pytest
 import torch
 
-from helpers import assert_close_rel, assert_mx_writeback, update_term_magnitudes
+from helpers import assert_close_rel, assert_mx_writeback, to_device, update_term_magnitudes
 from layer_quant_amd import _abi
 from oracle import mx_state as omx
 
@@ -55,8 +55,14 @@ CASES = _draw_cases(32, 1202)
 
 
 @pytest.mark.parametrize("i,c", CASES, ids=[f"case{i}" for i, _ in CASES])
-def test_mx_update_random(gpu, i, c):
-    print(f"[case {i}] {c}", flush=True)
+def test_mx_update_random(gpu, monkeypatch, i, c):
+    # the row kernel's layout: dt and A constant along head_dim, d_state 64/128/256, and in
+    # counter mode an offset that is a multiple of 16; the library must then take that kernel
+    rows = (c["head_dt"] and not c["a_rows"] and c["n"] != 96
+            and not (c["mode"] == 3 and c["off"] % 16 != 0))
+    if rows:
+        monkeypatch.setenv("LQ_MX_REQUIRE_ROWS", "1")
+    print(f"[case {i}] {'rows' if rows else 'general'} {c}", flush=True)
     g = torch.Generator().manual_seed(5000 + i)
     bsz, nh, p_, n, ng = c["bsz"], c["ng"] * c["ratio"], c["p"], c["n"], c["ng"]
     shape = (bsz, nh, p_, n)
@@ -83,7 +89,7 @@ def test_mx_update_random(gpu, i, c):
     uni = torch.rand(*shape, generator=g) if c["mode"] == 2 else None
     st = [torch.from_numpy(a).to(gpu) for a in (q, e, m)]
     out = torch.empty(bsz, nh, p_, dtype=DTYPES[c["odt"]], device=gpu)
-    dev = {k: (None if v is None else v.to(gpu)) for k, v in t.items()}
+    dev = {k: to_device(v, gpu) for k, v in t.items()}
     _abi.mx_state_update(*st, dev["x"], dev["dt"], dev["dt_bias"], dev["A"], dev["B"], dev["C"],
                          dev["D"], dev["z"], out, c["fb"], c["softplus"], c["mode"],
                          uniform=None if uni is None else uni.to(gpu), seed=c["seed"],

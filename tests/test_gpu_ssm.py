@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close_rel
+from helpers import assert_close_rel, to_device
 from hybrid_quant import mamba_state_8b_kernel as ms
 from layer_quant_amd import _abi
 from oracle import mx_state as omx
@@ -28,8 +28,9 @@ def _inputs(bsz, nh, p_, n, ng, seed, head_const=True, z=False, dt_zero=False):
         A = -torch.rand(nh, p_, n, generator=g)
         D = torch.randn(nh, p_, generator=g)
         dt_bias = torch.randn(nh, p_, generator=g) * 0.1
-    if dt_zero:
-        dt = torch.zeros_like(dt)
+    if dt_zero:  # zeros_like would give an expanded dt contiguous strides
+        dt = torch.zeros(*dt.shape[:-1], 1, dtype=dt.dtype).expand(dt.shape) if head_const \
+            else torch.zeros_like(dt)
     return dict(
         x=torch.randn(bsz, nh, p_, generator=g).to(torch.bfloat16),
         dt=dt, A=A, D=D, dt_bias=dt_bias,
@@ -41,14 +42,18 @@ def _inputs(bsz, nh, p_, n, ng, seed, head_const=True, z=False, dt_zero=False):
 
 @pytest.fixture(params=["rows", "general"])
 def path(request, monkeypatch):
-    """Run a model-layout test on the row kernel, and once more with the general kernel forced."""
+    """Run a model-layout test on the row kernel (the library refuses a call that would take the
+    general kernel), and once more with the general kernel forced."""
     if request.param == "general":
         monkeypatch.setenv("LQ_SSM_FORCE_GENERIC", "1")
+    else:
+        monkeypatch.setenv("LQ_SSM_REQUIRE_ROWS", "1")
     return request.param
 
 
 def _to(t, dev):
-    return {k: (None if v is None else v.to(dev)) for k, v in t.items()}
+    """Inputs on the device, expanded head scalars kept expanded (the model's layout)."""
+    return {k: to_device(v, dev) for k, v in t.items()}
 
 
 ULP = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10, torch.float32: 2.0 ** -23}
