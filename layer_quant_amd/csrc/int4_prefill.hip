@@ -624,7 +624,12 @@ extern "C" int lq_int4_prefill_attention(const lq_tensor* q, const lq_tensor* k_
   p.scale_sm = (float)(1.4426950408889634 / sqrt((double)D));
 
   hipStream_t st = (hipStream_t)stream;
-  if (prefill_mfma_ok(p)) {
+  const bool mfma = prefill_mfma_ok(p);
+  if (!mfma && env_flag("LQ_PREFILL_REQUIRE_MFMA")) {  // tests: the call must take the MFMA kernel
+    return fail(LQ_ERR_INVALID_ARG,
+                "LQ_PREFILL_REQUIRE_MFMA is set and this call takes the generic kernel");
+  }
+  if (mfma) {
     switch (PD / group_size) {
       case 4: launch_mfma<4>(p, st); break;
       case 2: launch_mfma<2>(p, st); break;

@@ -1,6 +1,9 @@
 """Shared checks of the test suite."""
 from __future__ import annotations
 
+import contextlib
+import os
+
 import numpy as np
 import torch
 
@@ -8,6 +11,38 @@ RTOL = 2e-3  # the attention output / updated state tolerance, fp32 accumulation
 
 # lines that tests register for the session's terminal summary (conftest.py prints them)
 REPORT: list[str] = []
+
+
+@contextlib.contextmanager
+def require_env(name: str, on: bool = True):
+    """Set the library's diagnostic switch `name` to 1 for the block (when `on`): with
+    LQ_ATTN_REQUIRE_FAST, LQ_PREFILL_REQUIRE_MFMA, LQ_MX_REQUIRE_ROWS or LQ_SSM_REQUIRE_ROWS set, a
+    call that would take the general kernel fails instead."""
+    prev = os.environ.get(name)
+    if on:
+        os.environ[name] = "1"
+    try:
+        yield
+    finally:
+        if on:
+            if prev is None:
+                del os.environ[name]
+            else:
+                os.environ[name] = prev
+
+
+def fast_attention_expected(q_dtype, head_dim: int, group_size: int, nrep: int) -> bool:
+    """The decode attention's MFMA gate for a contiguous packed cache: bf16 queries, head_dim
+    128, group 32/64/128, 1-16 query heads per KV head (a power of two) with
+    nrep * (128 / group) <= 16 MFMA columns."""
+    return (q_dtype == torch.bfloat16 and head_dim == 128 and group_size in (32, 64, 128)
+            and nrep in (1, 2, 4, 8, 16) and nrep * (128 // group_size) <= 16)
+
+
+def prefill_mfma_expected(q_dtype, head_dim: int, group_size: int) -> bool:
+    """The prefill's MFMA gate for a contiguous packed cache: bf16 queries, head_dim 128, group
+    32/64/128."""
+    return q_dtype == torch.bfloat16 and head_dim == 128 and group_size in (32, 64, 128)
 
 
 def to_device(t: torch.Tensor | None, device) -> torch.Tensor | None:

@@ -3,7 +3,7 @@ attention (MFMA fast path and generic path) is within 2e-3 of the float64 oracle
 import pytest
 import torch
 
-from helpers import assert_close_rel
+from helpers import assert_close_rel, fast_attention_expected, require_env
 from layer_quant_amd import _abi
 from hybrid_quant import int4_8b_attention as ia
 from oracle import int4_kv as oik
@@ -115,11 +115,13 @@ def _packed_cache(b, hkv, s, d, g, seed, cap=None):
 
 
 def _run_attention(gpu, cache, q, s, nrep, g, mask=None, out_dtype=torch.float32):
+    """One call; a call whose shape and dtype pass the MFMA gate must take the MFMA kernel."""
     dev = {k: v.to(gpu) for k, v in cache.items() if torch.is_tensor(v)}
     out = torch.empty(q.shape[0], q.shape[1], q.shape[-1], dtype=out_dtype, device=gpu)
-    _abi.int4_decode_attention(q.to(gpu), dev["k_packed"], dev["v_packed"], dev["k_scale"],
-                               dev["v_scale"], None if mask is None else mask.to(gpu), out, s,
-                               nrep, g)
+    with require_env("LQ_ATTN_REQUIRE_FAST", fast_attention_expected(q.dtype, q.shape[-1], g, nrep)):
+        _abi.int4_decode_attention(q.to(gpu), dev["k_packed"], dev["v_packed"], dev["k_scale"],
+                                   dev["v_scale"], None if mask is None else mask.to(gpu), out,
+                                   s, nrep, g)
     torch.cuda.synchronize()
     return out.cpu()
 
@@ -249,10 +251,11 @@ def test_attention_long_wave_ranges_masked(gpu, s, g):
                                                    (2, 2, 16, 777, 128, False),
                                                    (64, 8, 4, 1057, 64, True),
                                                    (8, 8, 4, 4133, 32, True)])
-def test_attention_repeats_bit_identical(gpu, b, hkv, nrep, s, g, masked):
+def test_attention_repeats_bit_identical(gpu, monkeypatch, b, hkv, nrep, s, g, masked):
     """The MFMA path's tile loads land in LDS behind explicit waits: repeated calls on the same
     inputs must give bit-identical outputs (a missing or short wait would read a tile early).
     The masked instance counts 7 loads per tile in its waits."""
+    monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
     d = 128
     gen = torch.Generator(device=gpu).manual_seed(b * 7 + s)
     kp = torch.randint(0, 256, (b, hkv, s, d // 2), dtype=torch.uint8, device=gpu, generator=gen)
@@ -275,9 +278,10 @@ def test_attention_repeats_bit_identical(gpu, b, hkv, nrep, s, g, masked):
     assert torch.isfinite(ref).all()
 
 
-def test_attention_concurrent_streams(gpu):
+def test_attention_concurrent_streams(gpu, monkeypatch):
     """Split-K calls in flight on two streams at once use separate workspaces (one per stream):
     each stream's results equal the same calls made one at a time on the default stream."""
+    monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
     b, hkv, nrep, d, g = 2, 8, 4, 128, 32
     cases = []
     for i, s in enumerate((3000, 1777)):
@@ -307,8 +311,9 @@ def test_attention_concurrent_streams(gpu):
 
 
 @pytest.mark.parametrize("b,s", [(64, 16384), (8, 4096)])
-def test_attention_full_size_sampled_heads(gpu, b, s):
+def test_attention_full_size_sampled_heads(gpu, monkeypatch, b, s):
     """BASELINE sizes: random packed cache built on the GPU, oracle on sampled (b, kv head)."""
+    monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
     hkv, nrep, d, g = 8, 4, 128, 32
     gen = torch.Generator(device=gpu).manual_seed(b + s)
     kp = torch.randint(0, 256, (b, hkv, s, d // 2), dtype=torch.uint8, device=gpu, generator=gen)

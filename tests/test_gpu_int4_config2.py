@@ -25,6 +25,13 @@ pytestmark = pytest.mark.gpu
 HKV, NREP, D = 8, 4, 128
 
 
+@pytest.fixture(autouse=True)
+def _mfma_kernel_required(monkeypatch):
+    """Every call here (bf16 queries, 4 query heads per KV head, group 32/64/128) must take the
+    MFMA kernel: the library refuses it otherwise."""
+    monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
+
+
 def _outlier_channels(gen, device, hkv=HKV, d=D, frac=0.01):
     """[hkv, d] multipliers: 8 on about `frac` of the channels, at least one per KV head."""
     chan = torch.rand(hkv, d, device=device, generator=gen) < frac

@@ -11,7 +11,7 @@ import random
 import pytest
 import torch
 
-from helpers import assert_close_rel
+from helpers import assert_close_rel, fast_attention_expected
 from layer_quant_amd import _abi
 from oracle import int4_kv as oik
 
@@ -65,7 +65,7 @@ def _mask(kind, b, s, gen):
 
 @pytest.mark.parametrize("i,b,hkv,nrep,s,g,mask_kind,qdt", CASES,
                          ids=[f"case{c[0]}" for c in CASES])
-def test_attention_random_shapes(gpu, i, b, hkv, nrep, s, g, mask_kind, qdt):
+def test_attention_random_shapes(gpu, monkeypatch, i, b, hkv, nrep, s, g, mask_kind, qdt):
     print(f"[case {i}] b={b} hkv={hkv} nrep={nrep} s={s} g={g} mask={mask_kind} q={qdt}",
           flush=True)
     gen = torch.Generator().manual_seed(1000 + i)
@@ -77,6 +77,8 @@ def test_attention_random_shapes(gpu, i, b, hkv, nrep, s, g, mask_kind, qdt):
     q = _activations((b, hkv * nrep, 1, D), gen).to(torch.bfloat16)
     if qdt == "f32":
         q = q.float()
+    if fast_attention_expected(q.dtype, D, g, nrep):  # then the MFMA kernel is required
+        monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
     mask = _mask(mask_kind, b, s, gen)
     ref = oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
                                cache["v_scale"], s, nrep, g, mask=mask)

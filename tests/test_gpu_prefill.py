@@ -4,7 +4,7 @@ bf16 outputs (the output rounding itself is 2^-9 relative)."""
 import pytest
 import torch
 
-from helpers import assert_close_rel
+from helpers import assert_close_rel, prefill_mfma_expected, require_env
 from layer_quant_amd import _abi
 from hybrid_quant import int4_8b_attention as ia
 from oracle import int4_kv as oik
@@ -31,8 +31,10 @@ def _packed_cache(b, hkv, s, d, g, seed, cap):
 def _run(gpu, cache, q, nrep, g, out_dtype=torch.float32):
     dev = {k: v.to(gpu) for k, v in cache.items() if torch.is_tensor(v)}
     out = torch.empty(*q.shape, dtype=out_dtype, device=gpu)
-    _abi.int4_prefill_attention(q.to(gpu), dev["k_packed"], dev["v_packed"], dev["k_scale"],
-                                dev["v_scale"], out, nrep, g)
+    # a call that passes the MFMA gate must take the MFMA kernel
+    with require_env("LQ_PREFILL_REQUIRE_MFMA", prefill_mfma_expected(q.dtype, q.shape[-1], g)):
+        _abi.int4_prefill_attention(q.to(gpu), dev["k_packed"], dev["v_packed"], dev["k_scale"],
+                                    dev["v_scale"], out, nrep, g)
     torch.cuda.synchronize()
     return out.cpu()
 
@@ -74,9 +76,10 @@ def test_prefill_generic_shapes(gpu, b, hkv, nrep, L, g, d):
     assert_close_rel(_run(gpu, cache, q, nrep, g), _oracle(cache, q, nrep, g))
 
 
-def test_prefill_strided_query_and_module_api(gpu):
-    """The model's query_states is a transposed view [B, L, Hq, D] -> [B, Hq, L, D];
-    _prefill_attention returns q's dtype like the reference (ia.py:600)."""
+def test_prefill_strided_query_and_module_api(gpu, monkeypatch):
+    """The model's query_states is a transposed view [B, L, Hq, D] -> [B, Hq, L, D], taken by the
+    MFMA kernel; _prefill_attention returns q's dtype like the reference (ia.py:600)."""
+    monkeypatch.setenv("LQ_PREFILL_REQUIRE_MFMA", "1")
     b, hkv, nrep, L, d, g = 2, 2, 4, 77, 128, 32
     cache = _packed_cache(b, hkv, L, d, g, 980, cap=128)
     q_bl = _activations((b, L, hkv * nrep, d), 981).transpose(1, 2)
@@ -87,10 +90,12 @@ def test_prefill_strided_query_and_module_api(gpu):
     assert_close_rel(out.float().cpu(), _oracle(cache, q_bl.contiguous(), nrep, g), rtol=8e-3)
 
 
-def test_prefill_full_size_sampled_rows(gpu):
+def test_prefill_full_size_sampled_rows(gpu, monkeypatch):
     """Nemotron-H attention layer at L = 16384 (32 q heads, 8 KV heads, group 32): sampled
     (head, position) rows against the oracle's decode over the row's prefix, and the last row
-    against the HIP decode kernel over the whole cache."""
+    against the HIP decode kernel over the whole cache (both calls on their MFMA kernels)."""
+    monkeypatch.setenv("LQ_PREFILL_REQUIRE_MFMA", "1")
+    monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
     b, hkv, nrep, L, d, g = 1, 8, 4, 16384, 128, 32
     gen = torch.Generator(device=gpu).manual_seed(16384)
     kp = torch.randint(0, 256, (b, hkv, L, d // 2), dtype=torch.uint8, device=gpu, generator=gen)

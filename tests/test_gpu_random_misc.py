@@ -18,7 +18,7 @@ import random
 import pytest
 import torch
 
-from helpers import assert_close_rel, to_device
+from helpers import assert_close_rel, prefill_mfma_expected, to_device
 from hybrid_quant import mamba_state_8b_kernel as ms
 from layer_quant_amd import _abi
 from oracle import int4_kv as oik
@@ -96,7 +96,7 @@ PREFILL_CASES = _prefill_cases(16, 88)
 
 @pytest.mark.parametrize("i,b,hkv,nrep,L,g,qdt,odt", PREFILL_CASES,
                          ids=[f"case{c[0]}" for c in PREFILL_CASES])
-def test_prefill_random(gpu, i, b, hkv, nrep, L, g, qdt, odt):
+def test_prefill_random(gpu, monkeypatch, i, b, hkv, nrep, L, g, qdt, odt):
     print(f"[prefill case {i}] b={b} hkv={hkv} nrep={nrep} L={L} g={g} q={qdt} out={odt}",
           flush=True)
     d = 128
@@ -109,6 +109,8 @@ def test_prefill_random(gpu, i, b, hkv, nrep, L, g, qdt, odt):
     q = _activations((b, hkv * nrep, L, d), gen).to(torch.bfloat16)
     if qdt == "f32":
         q = q.float()
+    if prefill_mfma_expected(q.dtype, d, g):  # then the MFMA kernel is required
+        monkeypatch.setenv("LQ_PREFILL_REQUIRE_MFMA", "1")
     ref = oik.prefill_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
                                 cache["v_scale"], nrep, g)
     dev = {n_: t.to(gpu) for n_, t in cache.items() if torch.is_tensor(t)}
