@@ -2,9 +2,10 @@
 """Decode-step benchmark of the quantized Nemotron-H-8B paths on one MI355X.
 
 One step = the quantized work of one decode step of the hybrid stack at batch 64, context 16384:
-  4 attention layers:  INT4 pack of the new K and V token (one lq_int4_pack_kv_pair call, as the
-                       module's _pack_kv_into_cache makes it) + q_len=1 decode attention
-                       over the packed cache (32 query / 8 KV heads, head_dim 128, group 32)
+  4 attention layers:  INT4 pack of the new K and V token into cache row S - 1 + q_len=1 decode
+                       attention over the packed cache (32 query / 8 KV heads, head_dim 128,
+                       group 32): one lq_int4_decode_attention_pack call, as the module's
+                       decode branch makes it (one kernel: the attention packs the token)
   24 Mamba2 layers:    fused MX4 selective-state update (128 heads x 64 x 128, 8 groups,
                        stochastic writeback from the counter generator)
 Every layer owns its own cache / state (about 8 GB in total), so no buffer is reused within a
@@ -227,7 +228,6 @@ def build_workload(torch, args, dev):
             k_new=torch.randn(B, hkv, 1, d, device=dev, generator=gen).to(torch.bfloat16),
             v_new=torch.randn(B, hkv, 1, d, device=dev, generator=gen).to(torch.bfloat16),
             out=torch.empty(B, hq, d, device=dev, dtype=torch.bfloat16),
-            pos=torch.full((1,), S - 1, dtype=torch.long, device=dev),
         )
         attn.append(layer)
     mamba = []
@@ -253,8 +253,8 @@ def build_workload(torch, args, dev):
         mamba.append(layer)
     torch.cuda.synchronize()
     sizes = dict(
-        attention=attention_bytes(B, hq, hkv, d, S, g),
-        pack=2 * pack_bytes(B, hkv, 1, d, g),  # K and V in one call
+        # the fused call: the attention's reads plus the new K and V token's pack
+        attention=attention_bytes(B, hq, hkv, d, S, g) + 2 * pack_bytes(B, hkv, 1, d, g),
         mx_update=mx_update_bytes(B, nh, p_, n, ng, format_bits=args.state_bits,
                                   layout=args.state_layout),
     )
@@ -273,15 +273,12 @@ def run_step(torch, args, attn, mamba, ev=None):
         else:
             ev.around(name, fn, calls)
 
-    # attention layers: pack then attend, per layer; each call timed by its own event pair
-    # (1-3 % of event overhead on the 215 us attention call)
+    # attention layers: pack the new token into row S - 1 and attend, one call per layer, each
+    # timed by its own event pair (1-3 % of event overhead on the 210 us call)
     for L in attn:
-        call("pack", lambda: _abi.int4_pack_kv_pair(L["k_new"], L["v_new"], L["k_packed"],
-                                                    L["v_packed"], L["k_scale"], L["v_scale"],
-                                                    L["pos"], g))
-        call("attention", lambda: _abi.int4_decode_attention(
-            L["q"], L["k_packed"], L["v_packed"], L["k_scale"], L["v_scale"], None, L["out"], S,
-            4, g))
+        call("attention", lambda: _abi.int4_decode_attention_pack(
+            L["q"], L["k_new"], L["v_new"], L["k_packed"], L["v_packed"], L["k_scale"],
+            L["v_scale"], None, L["out"], S, 4, g))
 
     # the Mamba layers' updates run back to back and are timed as one run per step: an event
     # pair around every 40 us update adds its own dispatch time (per-call events read 1-2.5 us
@@ -719,7 +716,6 @@ def main():
         kernels[name] = {"us": round(us, 2), "algorithmic_bytes": nbytes,
                          "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
                          "calls_per_step": {"attention": args.attn_layers,
-                                            "pack": args.attn_layers,
                                             "mx_update": args.mamba_layers}[name],
                          "per_call_us": ev.spread_us(name)}
         log(f"{name}: {us:.1f} us/call, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%})")
@@ -728,10 +724,10 @@ def main():
     workload = f"b{args.batch}_ctx{args.ctx}_g{args.group}_mx{args.state_bits}" + (
         "_compact" if args.state_layout == "compact" else "")
     roofline = {
-        "kernel": {"attention": "lq_int4_decode_attention (attn_fast_kernel, + attn_merge_kernel "
-                                "when split)",
+        "kernel": {"attention": "lq_int4_decode_attention_pack (attn_fast_kernel with the "
+                                "token's pack, + attn_merge_kernel when split)",
                    "mx_update": f"lq_mx_state_update (mx_update_rows_kernel MX{args.state_bits})",
-                   "pack": "lq_int4_pack_kv_pair"}[dominant],
+                   }[dominant],
         "bound": "hbm",
         "achieved": dk["GB_s"],
         "peak": PEAK_HBM_GBS,

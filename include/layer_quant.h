@@ -136,6 +136,26 @@ int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
                              void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * One decode step of an attention layer: lq_int4_pack_kv_pair of the new token's k_new, v_new
+ * [B, Hkv, 1, D] (f32/f16/bf16, any strides) into cache row seq_len - 1, then
+ * lq_int4_decode_attention over keys [0, seq_len) -- the same checks, the same cache bytes and
+ * the same output as those two calls. On the MFMA path (bf16 q, head_dim 128, group 32/64/128)
+ * it is one launch: the wave that attends to key seq_len - 1 packs the token, writes it to the
+ * cache and uses its own bytes for that key; elsewhere the two kernels run in turn. The workspace
+ * is sized by lq_int4_decode_attention_workspace.
+ * Replaces the decode branch of the reference's patched forward, _pack_kv_into_cache followed by
+ * _decode_attention (reference hybrid_quant/int4_8b_attention.py:678-690; the kernels at :32-111
+ * and :254-402).
+ */
+int lq_int4_decode_attention_pack(const lq_tensor* q, const lq_tensor* k_new,
+                                  const lq_tensor* v_new, const lq_tensor* k_packed,
+                                  const lq_tensor* v_packed, const lq_tensor* k_scale,
+                                  const lq_tensor* v_scale, const lq_tensor* mask,
+                                  const lq_tensor* out, int64_t seq_len, int num_key_value_groups,
+                                  int group_size, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/*
  * lq_int4_decode_attention without a workspace: the same validation, kernels and results, with
  * the split-K partials in a static per-device buffer inside the library
  * (LQ_DECODE_ATTENTION_NOALLOC_SCRATCH_BYTES, 8 MiB on every GPU the library runs on, held until

@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "lq_int4_pack_kv_pair",
     "lq_int4_decode_attention_workspace",
     "lq_int4_decode_attention",
+    "lq_int4_decode_attention_pack",
     "lq_int4_decode_attention_noalloc",
     "lq_int4_prefill_attention",
     "lq_mx_encode",
@@ -90,6 +91,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.lq_int4_decode_attention_workspace.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int]
     lib.lq_int4_decode_attention.restype = ctypes.c_int
     lib.lq_int4_decode_attention.argtypes = [_P] * 7 + [
+        ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+        ctypes.c_void_p]
+    lib.lq_int4_decode_attention_pack.restype = ctypes.c_int
+    lib.lq_int4_decode_attention_pack.argtypes = [_P] * 9 + [
         ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
         ctypes.c_void_p]
     lib.lq_int4_decode_attention_noalloc.restype = ctypes.c_int
@@ -245,6 +250,28 @@ def int4_decode_attention(q: torch.Tensor, k_packed: torch.Tensor, v_packed: tor
         desc(out), int(seq_len), int(num_key_value_groups), int(group_size),
         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream)
     check(rc, "lq_int4_decode_attention")
+    return out
+
+
+def int4_decode_attention_pack(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                               k_packed: torch.Tensor, v_packed: torch.Tensor,
+                               k_scale: torch.Tensor, v_scale: torch.Tensor,
+                               mask: torch.Tensor | None, out: torch.Tensor, seq_len: int,
+                               num_key_value_groups: int, group_size: int) -> torch.Tensor:
+    """int4_pack_kv_pair of the new token k_new, v_new [B, Hkv, 1, D] into cache row
+    seq_len - 1, then int4_decode_attention over keys [0, seq_len) -> out; one launch on the MFMA
+    path."""
+    dev = _require_gpu(q, k_new, v_new, k_packed, v_packed, k_scale, v_scale, mask, out)
+    stream = _stream(dev)
+    need = int4_decode_attention_workspace(q.shape[0], q.shape[1], k_packed.shape[1],
+                                           q.shape[-1], seq_len, group_size)
+    ws = _workspace.get(dev, stream, need)
+    rc = lib().lq_int4_decode_attention_pack(
+        desc(q), desc(k_new), desc(v_new), desc(k_packed), desc(v_packed), desc(k_scale),
+        desc(v_scale), desc(mask), desc(out), int(seq_len), int(num_key_value_groups),
+        int(group_size), None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+        stream)
+    check(rc, "lq_int4_decode_attention_pack")
     return out
 
 

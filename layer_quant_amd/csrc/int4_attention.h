@@ -26,6 +26,10 @@ struct AttnParams {
   int nsplit;     // workgroup splits along the keys
   int64_t chunk;  // keys per workgroup split
   float scale_sm; // log2(e) / sqrt(D)
+  // fused pack (lq_int4_decode_attention_pack, MFMA path): the new token's K and V rows
+  // [B, Hkv, D] (strides of b, h, d) are packed into cache row S - 1 inside the kernel
+  View knew, vnew;
+  int pack;
 };
 
 struct SplitPlan {

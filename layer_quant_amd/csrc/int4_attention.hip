@@ -15,6 +15,7 @@
 #include <mutex>
 
 #include "int4_attention.h"
+#include "int4_quant.h"
 
 namespace lq {
 
@@ -289,11 +290,17 @@ struct PartialsBuffer {
   bool use_scratch;
 };
 
+// The new token's K and V rows for lq_int4_decode_attention_pack (NULL: attention only).
+struct NewToken {
+  const lq_tensor* k;
+  const lq_tensor* v;
+};
+
 static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
                             const lq_tensor* v_packed, const lq_tensor* k_scale,
                             const lq_tensor* v_scale, const lq_tensor* mask, const lq_tensor* out,
                             int64_t seq_len, int num_key_value_groups, int group_size,
-                            PartialsBuffer buf, void* stream);
+                            PartialsBuffer buf, void* stream, NewToken tok = {nullptr, nullptr});
 
 }  // namespace lq
 
@@ -323,6 +330,23 @@ extern "C" int lq_int4_decode_attention(const lq_tensor* q, const lq_tensor* k_p
                           PartialsBuffer{workspace, workspace_bytes, false}, stream);
 }
 
+extern "C" int lq_int4_decode_attention_pack(const lq_tensor* q, const lq_tensor* k_new,
+                                             const lq_tensor* v_new, const lq_tensor* k_packed,
+                                             const lq_tensor* v_packed, const lq_tensor* k_scale,
+                                             const lq_tensor* v_scale, const lq_tensor* mask,
+                                             const lq_tensor* out, int64_t seq_len,
+                                             int num_key_value_groups, int group_size,
+                                             void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  if (k_new == nullptr || v_new == nullptr) {
+    return fail(LQ_ERR_INVALID_ARG, "k_new and v_new are required");
+  }
+  return decode_attention(q, k_packed, v_packed, k_scale, v_scale, mask, out, seq_len,
+                          num_key_value_groups, group_size,
+                          PartialsBuffer{workspace, workspace_bytes, false}, stream,
+                          NewToken{k_new, v_new});
+}
+
 extern "C" int lq_int4_decode_attention_noalloc(const lq_tensor* q, const lq_tensor* k_packed,
                                                 const lq_tensor* v_packed,
                                                 const lq_tensor* k_scale,
@@ -341,7 +365,7 @@ static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
                             const lq_tensor* v_packed, const lq_tensor* k_scale,
                             const lq_tensor* v_scale, const lq_tensor* mask, const lq_tensor* out,
                             int64_t seq_len, int num_key_value_groups, int group_size,
-                            PartialsBuffer buf, void* stream) {
+                            PartialsBuffer buf, void* stream, NewToken tok) {
   int rc;
   if (q == nullptr) return fail(LQ_ERR_INVALID_ARG, "q: descriptor is NULL");
   const int qdim = q->ndim;
@@ -402,6 +426,16 @@ static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
                   (long long)B);
     }
   }
+  if (tok.k != nullptr) {
+    // the token tensors as lq_int4_pack_kv_pair checks them, one token into row seq_len - 1
+    if ((rc = pack_pair_at(tok.k, tok.v, k_packed, v_packed, k_scale, v_scale, seq_len - 1,
+                           group_size, false, nullptr, "")) != LQ_OK) {
+      return rc;
+    }
+    if (tok.k->shape[2] != 1 || tok.v->shape[2] != 1) {
+      return fail(LQ_ERR_INVALID_ARG, "k_new and v_new must hold one token ([B, Hkv, 1, D])");
+    }
+  }
   if (B == 0 || Hq == 0) return LQ_OK;
 
   AttnParams p{};
@@ -441,6 +475,15 @@ static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
     return fail(LQ_ERR_INVALID_ARG,
                 "LQ_ATTN_REQUIRE_FAST is set and this call takes the generic kernel");
   }
+  if (tok.k != nullptr && fast) {  // the MFMA kernel packs the token itself
+    auto row_view = [](const lq_tensor* t) {
+      View v{t->data, t->dtype, {t->stride[0], t->stride[1], t->stride[3], 0}};
+      return v;
+    };
+    p.knew = row_view(tok.k);
+    p.vnew = row_view(tok.v);
+    p.pack = 1;
+  }
   const SplitPlan sp = fast ? plan_fast(B, Hkv, seq_len) : plan_generic(B, Hq, seq_len);
   p.nsplit = sp.nsplit;
   p.chunk = sp.chunk;
@@ -468,6 +511,12 @@ static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
     carve_workspace(p, buf.workspace);
   }
 
+  if (tok.k != nullptr && !fast) {  // the generic kernel reads row seq_len - 1: pack it first
+    if ((rc = pack_pair_at(tok.k, tok.v, k_packed, v_packed, k_scale, v_scale, seq_len - 1,
+                           group_size, true, st, "lq_int4_decode_attention_pack (pack)")) != LQ_OK) {
+      return rc;
+    }
+  }
   if (fast) {
     if ((rc = launch_fast(p, st)) != LQ_OK) return rc;
   } else {

@@ -38,6 +38,7 @@
 #include <stdlib.h>
 
 #include "int4_attention.h"
+#include "int4_quant.h"
 
 namespace lq {
 
@@ -315,6 +316,28 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   const float csm = p.scale_sm;  // raw scores -> log2 units
   const float inv_csm = 1.0f / csm;
 
+  // Fused pack (lq_int4_decode_attention_pack): the wave whose dealt tiles hold key S - 1 (its
+  // last tile) loads the new token's K and V values here (lane j: dims 2j and 2j + 1) and packs
+  // them when it reaches that tile, after the tile's wait (a full one, the last tile having no
+  // loads behind it): the pack kernel's arithmetic, written to cache row S - 1 and over the key's
+  // row in the LDS tile, whichever version the tile's loads read. (The fast path's caches have
+  // 64-byte rows and contiguous scales, so the row is indexed directly.)
+  constexpr int GH = FAST_D / (2 * G);  // lanes per quantisation group
+  int pack_i = -1;                      // the wave's tile index holding key S - 1, or -1
+  float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f;
+  if (p.pack && t1 == S) {
+    const int tile = (S - 1 - t0) / TILE;
+    if (tile % WAVES == wave) {
+      pack_i = tile / WAVES;
+      const int64_t kx = b * p.knew.s[0] + (int64_t)kvh * p.knew.s[1];
+      const int64_t vx = b * p.vnew.s[0] + (int64_t)kvh * p.vnew.s[1];
+      kx0 = load_float(p.knew.data, p.knew.dtype, kx + 2 * lane * p.knew.s[2]);
+      kx1 = load_float(p.knew.data, p.knew.dtype, kx + (2 * lane + 1) * p.knew.s[2]);
+      vx0 = load_float(p.vnew.data, p.vnew.dtype, vx + 2 * lane * p.vnew.s[2]);
+      vx1 = load_float(p.vnew.data, p.vnew.dtype, vx + (2 * lane + 1) * p.vnew.s[2]);
+    }
+  }
+
   // QK A-row i of a 16-key half is key 4 (i & 3) + (i >> 2), so that output row 4q + r (held by
   // lane group q) is key 4r + q, and lane group q's 8 keys of the tile are q + 4e (e = 4t + r).
   const int krow = 4 * (c16 & 3) + (c16 >> 2);
@@ -336,9 +359,27 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
     else wait_loads<0>();
   };
 
-  auto process = [&](const int i, const TileLds& B) {
+  auto process = [&](const int i, TileLds& B) {
     const int tb = tile_key(i);
     wait_tile(i);
+    if (i == pack_i) {  // key S - 1 of this tile: the fused pack (LDS layout as in TileLds)
+      float kscl, vscl;
+      const uint32_t kbyte = int4_quantize_pair<GH>(kx0, kx1, kscl);
+      const uint32_t vbyte = int4_quantize_pair<GH>(vx0, vx1, vscl);
+      const int key = S - 1 - tb;
+      const int hk = key >> 4;
+      const int r = key & 15;
+      ((uint8_t*)&B.k[hk][4 * r + ((lane >> 4) ^ ((r >> 2) & 3))])[lane & 15] = (uint8_t)kbyte;
+      ((uint8_t*)&B.v[hk][0])[r * 64 + lane] = (uint8_t)vbyte;
+      const_cast<uint8_t*>(R.kb)[(int64_t)(S - 1) * 64 + lane] = (uint8_t)kbyte;
+      const_cast<uint8_t*>(R.vb)[(int64_t)(S - 1) * 64 + lane] = (uint8_t)vbyte;
+      if ((lane & (GH - 1)) == 0) {
+        B.ks[key * G + lane / GH] = kscl;
+        B.vs[key * G + lane / GH] = vscl;
+        const_cast<float*>(R.ksb)[(int64_t)(S - 1) * G + lane / GH] = kscl;
+        const_cast<float*>(R.vsb)[(int64_t)(S - 1) * G + lane / GH] = vscl;
+      }
+    }
     // scores S^T (keys x columns) in raw units: two 16-key halves, 4 chunks each
     f32x4_t sacc[2];
     sacc[0] = f32x4_t{cinit, cinit, cinit, cinit};

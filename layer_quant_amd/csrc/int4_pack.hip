@@ -9,6 +9,7 @@
 // two tensors (blockIdx.y picks one): lq_int4_pack_kv_pair packs a layer's K and V in one launch.
 #include <algorithm>
 
+#include "int4_quant.h"
 #include "lq_common.h"
 
 namespace lq {
@@ -19,8 +20,9 @@ struct PackParams {
   int64_t ps[4];  // [B, Hkv, cap, D/2]
   float* scale;
   int64_t ss[4];  // [B, Hkv, cap, D/g]
-  const int64_t* positions;
+  const int64_t* positions;  // NULL: token t goes to row fixed_pos + t
   int64_t pos_stride;
+  int64_t fixed_pos;
   int B, H, T, D, g;
   int64_t cap;
 };
@@ -50,16 +52,11 @@ __global__ __launch_bounds__(256) void int4_pack_lanes_kernel(PackPair pair) {
   const int64_t xrow = b * p.x.s[0] + h * p.x.s[1] + t * p.x.s[2];
   const float v0 = load_float(p.x.data, p.x.dtype, xrow + (2 * j) * p.x.s[3]);
   const float v1 = load_float(p.x.data, p.x.dtype, xrow + (2 * j + 1) * p.x.s[3]);
-  float amax = fmaxf(fabsf(v0), fabsf(v1));
-#pragma unroll
-  for (int o = GH >> 1; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-  const float scale = fmaxf(amax / 7.0f, 1.0e-8f);
-  const int q0 = min(max((int)rintf(v0 / scale), -8), 7);
-  const int q1 = min(max((int)rintf(v1 / scale), -8), 7);
-  const int64_t pos = p.positions[t * p.pos_stride];
+  float scale;
+  const uint32_t byte = int4_quantize_pair<GH>(v0, v1, scale);
+  const int64_t pos = p.positions != nullptr ? p.positions[t * p.pos_stride] : p.fixed_pos + t;
   if (!in || pos < 0 || pos >= p.cap) return;
-  p.packed[b * p.ps[0] + h * p.ps[1] + pos * p.ps[2] + j * p.ps[3]] =
-      (uint8_t)(((q1 & 15) << 4) | (q0 & 15));
+  p.packed[b * p.ps[0] + h * p.ps[1] + pos * p.ps[2] + j * p.ps[3]] = (uint8_t)byte;
   if ((j & (GH - 1)) == 0) {
     p.scale[b * p.ss[0] + h * p.ss[1] + pos * p.ss[2] + (j / GH) * p.ss[3]] = scale;
   }
@@ -77,7 +74,7 @@ __global__ __launch_bounds__(256) void int4_pack_kernel(PackPair pair) {
   r /= p.T;
   const int h = (int)(r % p.H);
   const int b = (int)(r / p.H);
-  const int64_t pos = p.positions[t * p.pos_stride];
+  const int64_t pos = p.positions != nullptr ? p.positions[t * p.pos_stride] : p.fixed_pos + t;
   if (pos < 0 || pos >= p.cap) return;
 
   const int64_t xrow = b * p.x.s[0] + h * p.x.s[1] + t * p.x.s[2];
@@ -107,14 +104,19 @@ using namespace lq;
 
 namespace {
 
-// Validate one (x, packed, scale) triple against positions and fill its launch parameters.
+// Validate one (x, packed, scale) triple against positions (a device tensor, or NULL for the
+// rows fixed_pos, fixed_pos + 1, ...) and fill its launch parameters.
 int make_pack_params(const lq_tensor* x, const lq_tensor* packed, const lq_tensor* scale,
-                     const lq_tensor* positions, int group_size, PackParams& p) {
+                     const lq_tensor* positions, int group_size, PackParams& p,
+                     int64_t fixed_pos = 0) {
   int rc;
   if ((rc = check_tensor(x, "x", 4, true)) != LQ_OK) return rc;
   if ((rc = check_tensor(packed, "packed", 4, false, LQ_U8)) != LQ_OK) return rc;
   if ((rc = check_tensor(scale, "scale", 4, false, LQ_F32)) != LQ_OK) return rc;
-  if ((rc = check_tensor(positions, "positions", 1, false, LQ_I64)) != LQ_OK) return rc;
+  if (positions != nullptr &&
+      (rc = check_tensor(positions, "positions", 1, false, LQ_I64)) != LQ_OK) {
+    return rc;
+  }
   const int64_t B = x->shape[0], H = x->shape[1], T = x->shape[2], D = x->shape[3];
   if (group_size <= 0 || group_size % 2 != 0) {
     return fail(LQ_ERR_INVALID_ARG, "group_size=%d must be even for INT4 packing", group_size);
@@ -133,9 +135,13 @@ int make_pack_params(const lq_tensor* x, const lq_tensor* packed, const lq_tenso
     return fail(LQ_ERR_INVALID_ARG, "scale must be [%lld, %lld, %lld, %lld]", (long long)B,
                 (long long)H, (long long)cap, (long long)(D / group_size));
   }
-  if (positions->shape[0] != T) {
+  if (positions != nullptr && positions->shape[0] != T) {
     return fail(LQ_ERR_INVALID_ARG, "positions has %lld entries for q_len=%lld",
                 (long long)positions->shape[0], (long long)T);
+  }
+  if (positions == nullptr && (fixed_pos < 0 || fixed_pos + T > cap)) {
+    return fail(LQ_ERR_INVALID_ARG, "rows %lld .. %lld outside the cache capacity %lld",
+                (long long)fixed_pos, (long long)(fixed_pos + T - 1), (long long)cap);
   }
   p = PackParams{};
   p.x = make_view(x);
@@ -145,8 +151,9 @@ int make_pack_params(const lq_tensor* x, const lq_tensor* packed, const lq_tenso
     p.ps[i] = packed->stride[i];
     p.ss[i] = scale->stride[i];
   }
-  p.positions = (const int64_t*)positions->data;
-  p.pos_stride = positions->stride[0];
+  p.positions = positions != nullptr ? (const int64_t*)positions->data : nullptr;
+  p.pos_stride = positions != nullptr ? positions->stride[0] : 0;
+  p.fixed_pos = fixed_pos;
   p.B = (int)B;
   p.H = (int)H;
   p.T = (int)T;
@@ -214,3 +221,21 @@ extern "C" int lq_int4_pack_kv_pair(const lq_tensor* k, const lq_tensor* v,
   }
   return launch_pack(pair, 2, group_size, (hipStream_t)stream, "lq_int4_pack_kv_pair");
 }
+
+namespace lq {
+
+int pack_pair_at(const lq_tensor* k, const lq_tensor* v, const lq_tensor* k_packed,
+                 const lq_tensor* v_packed, const lq_tensor* k_scale, const lq_tensor* v_scale,
+                 int64_t row, int group_size, bool launch, hipStream_t stream, const char* what) {
+  PackPair pair{};
+  int rc;
+  if ((rc = make_pack_params(k, k_packed, k_scale, nullptr, group_size, pair.pp[0], row)) != LQ_OK) {
+    return rc;
+  }
+  if ((rc = make_pack_params(v, v_packed, v_scale, nullptr, group_size, pair.pp[1], row)) != LQ_OK) {
+    return rc;
+  }
+  return launch ? launch_pack(pair, 2, group_size, stream, what) : LQ_OK;
+}
+
+}  // namespace lq

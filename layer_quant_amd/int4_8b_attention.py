@@ -166,6 +166,26 @@ def _decode_attention(query_states: torch.Tensor, cache: Int4KVLayerCache, seq_l
     return out
 
 
+def _pack_and_decode_attention(query_states: torch.Tensor, key_states: torch.Tensor,
+                               value_states: torch.Tensor, cache: Int4KVLayerCache,
+                               seq_len: int, num_key_value_groups: int, group_size: int,
+                               attention_mask: torch.Tensor | None = None) -> torch.Tensor:
+    """_pack_kv_into_cache of the step's one token into row seq_len - 1, then _decode_attention
+    over rows [0, seq_len): the reference's decode branch (ia.py:678-690) as one library call,
+    which on the MFMA path is one kernel launch. Same cache bytes, length and output."""
+    batch, n_heads, q_len, head_dim = query_states.shape
+    if q_len != 1 or key_states.shape[2] != 1:
+        raise ValueError(f"Fused INT4 decode attention expects q_len=1, got {q_len}")
+    out = torch.empty((batch, n_heads, head_dim), device=query_states.device,
+                      dtype=query_states.dtype)
+    mask = _decode_attention_mask(attention_mask, batch, seq_len, query_states.device)
+    _abi.int4_decode_attention_pack(query_states, key_states, value_states, cache.k_packed,
+                                    cache.v_packed, cache.k_scale, cache.v_scale, mask, out,
+                                    seq_len, num_key_value_groups, group_size)
+    cache.length = max(cache.length, seq_len)
+    return out
+
+
 def _prefill_attention(query_states: torch.Tensor, cache: Int4KVLayerCache,
                        num_key_value_groups: int, group_size: int) -> torch.Tensor:
     """Causal attention of q [B, Hq, L, D] over cache rows [0, L): position t attends to rows
@@ -210,14 +230,15 @@ def _forward_fused_int4_kv(self, hidden_states, attention_mask=None, position_id
     layer_cache = _ensure_layer_cache(past_key_value, self.layer_idx, bsz,
                                       self.num_key_value_heads, required_len, self.head_dim,
                                       group_size, hidden_states.device)
-    _pack_kv_into_cache(layer_cache, key_states, value_states, positions, group_size)
-
     if q_len == 1:
-        attn = _decode_attention(query_states, layer_cache, required_len,
-                                 self.num_key_value_groups, group_size,
-                                 attention_mask=attention_mask)
+        # the token's row is required_len - 1 (positions holds that one value)
+        attn = _pack_and_decode_attention(query_states, key_states, value_states, layer_cache,
+                                          required_len, self.num_key_value_groups, group_size,
+                                          attention_mask=attention_mask)
         attn = attn.reshape(bsz, q_len, self.hidden_size)
         return self.o_proj(attn), None, past_key_value
+
+    _pack_kv_into_cache(layer_cache, key_states, value_states, positions, group_size)
 
     key_full = self._int4_kv_repeat_kv(key_states, self.num_key_value_groups)
     value_full = self._int4_kv_repeat_kv(value_states, self.num_key_value_groups)

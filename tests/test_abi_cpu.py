@@ -109,6 +109,34 @@ def test_attention_rejects_bad_arguments():
                                         0, None) == _abi.LQ_ERR_WORKSPACE
 
 
+def test_fused_pack_attention_rejects_bad_arguments():
+    """lq_int4_decode_attention_pack checks its token tensors as lq_int4_pack_kv_pair does (one
+    token, into row seq_len - 1) and the rest as lq_int4_decode_attention does."""
+    lib = _abi.lib()
+    f = lib.lq_int4_decode_attention_pack
+    kp = _fake((2, 8, 64, 64), torch.uint8)
+    ks = _fake((2, 8, 64, 4), torch.float32)
+    out = _fake((2, 32, 128), torch.bfloat16)
+    q = _fake((2, 32, 1, 128), torch.bfloat16)
+    kn = _fake((2, 8, 1, 128), torch.bfloat16)
+    assert f(q, None, kn, kp, kp, ks, ks, None, out, 10, 4, 32, None, 0,
+             None) == _abi.LQ_ERR_INVALID_ARG
+    assert "k_new" in _abi.last_error()
+    two = _fake((2, 8, 2, 128), torch.bfloat16)
+    assert f(q, two, two, kp, kp, ks, ks, None, out, 10, 4, 32, None, 0,
+             None) == _abi.LQ_ERR_INVALID_ARG
+    assert "one token" in _abi.last_error()
+    heads = _fake((2, 4, 1, 128), torch.bfloat16)
+    assert f(q, heads, kn, kp, kp, ks, ks, None, out, 10, 4, 32, None, 0,
+             None) == _abi.LQ_ERR_INVALID_ARG
+    assert f(q, kn, kn, kp, kp, ks, ks, None, out, 65, 4, 32, None, 0,
+             None) == _abi.LQ_ERR_INVALID_ARG
+    assert "capacity" in _abi.last_error()
+    ints = _fake((2, 8, 1, 128), torch.int32)
+    assert f(q, kn, ints, kp, kp, ks, ks, None, out, 10, 4, 32, None, 0,
+             None) == _abi.LQ_ERR_INVALID_ARG
+
+
 def test_prefill_rejects_bad_arguments():
     lib = _abi.lib()
     kp = _fake((2, 8, 64, 64), torch.uint8)

@@ -1,6 +1,7 @@
-"""A decode step captured in a HIP graph (through torch.cuda.CUDAGraph): fused K+V pack, decode
-attention with split-K partials in the per-stream workspace, and an MX4 state update with the
-counter generator. Three replays, with eager GPU work and synchronizations between them, each
+"""A decode step captured in a HIP graph (through torch.cuda.CUDAGraph): the attention layer as
+the fused K+V pack and the decode attention, or as the one call that packs and attends
+(lq_int4_decode_attention_pack), with split-K partials in the per-stream workspace, and an MX4
+state update with the counter generator. Three replays, with eager GPU work and synchronizations between them, each
 match the same calls run eagerly, bit for bit. None of these entry points records a memset."""
 import pytest
 import torch
@@ -48,8 +49,14 @@ def _make_state(gpu, seed):
 
 def _step(t):
     s, nrep, g = t["dims"]
-    _abi.int4_pack_kv_pair(t["k_new"], t["v_new"], t["kp"], t["vp"], t["ks"], t["vs"], t["pos"], g)
-    _abi.int4_decode_attention(t["q"], t["kp"], t["vp"], t["ks"], t["vs"], None, t["att"], s, nrep, g)
+    if t["fused"]:
+        _abi.int4_decode_attention_pack(t["q"], t["k_new"], t["v_new"], t["kp"], t["vp"], t["ks"],
+                                        t["vs"], None, t["att"], s, nrep, g)
+    else:
+        _abi.int4_pack_kv_pair(t["k_new"], t["v_new"], t["kp"], t["vp"], t["ks"], t["vs"],
+                               t["pos"], g)
+        _abi.int4_decode_attention(t["q"], t["kp"], t["vp"], t["ks"], t["vs"], None, t["att"], s,
+                                   nrep, g)
     _abi.mx_state_update(*t["st"], t["x"], t["dt"], t["dt_bias"], t["A"], t["B"], t["C"], t["D"],
                          None, t["y"], 4, True, _abi.ROUND_SR_COUNTER, seed=1234, rng_offset=4096)
 
@@ -63,8 +70,10 @@ def _restore(t, snap):
         dst.copy_(src)
 
 
-def test_decode_step_graph_replays_match_eager(gpu):
+@pytest.mark.parametrize("fused", [False, True], ids=["pack+attention", "fused"])
+def test_decode_step_graph_replays_match_eager(gpu, fused):
     t = _make_state(gpu, 2024)
+    t["fused"] = fused
     start = _snapshot(t)
     eager = []
     for _ in range(3):  # the state update feeds the next step's state
