@@ -9,6 +9,9 @@
 // Scores follow the reference: s_n = (q . k_n) * log2(e)/sqrt(D) (+ mask_n), exp2-domain online
 // softmax; keys at or beyond the mask length get -inf. Splits write (m, l, acc[D]) partials into
 // the caller's workspace and attn_merge_kernel combines them; a single split writes out directly.
+// lq_int4_decode_attention_pack first packs the new token into cache row seq_len - 1 (the
+// reference's _pack_kv_into_cache at :477-515): inside attn_fast_kernel on the MFMA path, by the
+// pack kernel before the generic one otherwise.
 #include <math.h>
 
 #include <atomic>

@@ -11,6 +11,11 @@
 // i+1 and i+2 are in flight, with no registers held for them. This replaced a ring of register
 // tiles (3 x 24 VGPRs per lane, V passed through LDS for its transpose anyway).
 //
+// Decode-token pack (lq_int4_decode_attention_pack). The wave whose last tile holds key S - 1
+// quantises the new token's K and V rows with the pack kernel's code, writes them to cache row
+// S - 1 and over that key's row in its LDS tile: one launch per layer instead of a pack launch
+// and the attention.
+//
 // MFMA v_mfma_f32_16x16x32_bf16, D[16x16] += A[16x32] * B[32x16]. Lane l holds A row l%16 and
 // B column l%16, each with K slots 8*(l/16) .. +7, and D rows 4*(l/16) .. +3 of column l%16.
 //
