@@ -100,11 +100,13 @@ __device__ __forceinline__ float word_elem(uint32_t w, uint32_t shift, int dtype
 
 // Element at a wave-uniform address, read by a scalar load of the aligned 32-bit word holding it
 // (a 4-byte aligned word never crosses a page, so it stays inside the allocation's pages).
-__device__ __forceinline__ float uniform_elem(const char* addr, int dtype) {
+__device__ __forceinline__ uint32_t uniform_word(const char* addr) {
   typedef const __attribute__((address_space(4))) uint32_t* cword_t;
-  const uintptr_t a = (uintptr_t)addr;
-  const uint32_t w = *(cword_t)(a & ~(uintptr_t)3);
-  return word_elem(w, (uint32_t)(a & 2u) * 8u, dtype);
+  return *(cword_t)((uintptr_t)addr & ~(uintptr_t)3);
+}
+
+__device__ __forceinline__ float uniform_elem(const char* addr, int dtype) {
+  return word_elem(uniform_word(addr), (uint32_t)((uintptr_t)addr & 2u) * 8u, dtype);
 }
 
 // Row-sum over the 2^BPR_LOG2 adjacent lanes of a state row with DPP moves: quad swaps, then the
@@ -156,10 +158,20 @@ struct HeadScalars {
 template <class Params>
 __device__ __forceinline__ HeadScalars head_scalars(const Params& p, int b, int h) {
   HeadScalars s;
-  float dtv = uniform_elem(vbase(p.dt, b, h), p.dt.dtype);
-  const float dtb = uniform_elem(vbase(p.dtb, h, 0), p.dtb.dtype);
-  const float av = uniform_elem(vbase(p.A, h, 0), p.A.dtype);
-  s.D = uniform_elem(vbase(p.D, h, 0), p.D.dtype);
+  // all four words are loaded before any dtype conversion (a branch), so that the loads go out
+  // together instead of one memory round trip after another
+  const char* a_dt = vbase(p.dt, b, h);
+  const char* a_dtb = vbase(p.dtb, h, 0);
+  const char* a_A = vbase(p.A, h, 0);
+  const char* a_D = vbase(p.D, h, 0);
+  uint32_t w_dt = uniform_word(a_dt), w_dtb = uniform_word(a_dtb);
+  uint32_t w_A = uniform_word(a_A), w_D = uniform_word(a_D);
+  asm volatile("" : "+s"(w_dt), "+s"(w_dtb), "+s"(w_A), "+s"(w_D));  // one wait for all four
+  auto sh = [](const char* a) { return (uint32_t)((uintptr_t)a & 2u) * 8u; };
+  float dtv = word_elem(w_dt, sh(a_dt), p.dt.dtype);
+  const float dtb = word_elem(w_dtb, sh(a_dtb), p.dtb.dtype);
+  const float av = word_elem(w_A, sh(a_A), p.A.dtype);
+  s.D = word_elem(w_D, sh(a_D), p.D.dtype);
   if (p.has_dtb) dtv += dtb;
   if (p.softplus) dtv = dtv <= 20.0f ? __logf(1.0f + __expf(dtv)) : dtv;
   s.dt = dtv;
