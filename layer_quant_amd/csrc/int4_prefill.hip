@@ -219,7 +219,24 @@ void prefill_mfma_kernel(PrefillParams p) {
     float mx[G];
 #pragma unroll
     for (int m = 0; m < G; ++m) mx[m] = 0.0f;
-    for (int k = tid; k < gend; k += 256) {
+    // eight keys' scales in flight per thread: one key per iteration waited out a full memory
+    // round trip each time (64 of them for a workgroup at the end of a 16K-token prompt)
+    constexpr int PRE = 8;
+    int k = tid;
+    for (; k + (PRE - 1) * 256 < gend; k += PRE * 256) {
+      float v[PRE][G];
+#pragma unroll
+      for (int u = 0; u < PRE; ++u) {
+#pragma unroll
+        for (int m = 0; m < G; ++m) v[u][m] = vsb[(int64_t)(k + u * 256) * G + m];
+      }
+#pragma unroll
+      for (int u = 0; u < PRE; ++u) {
+#pragma unroll
+        for (int m = 0; m < G; ++m) mx[m] = fmaxf(mx[m], v[u][m]);
+      }
+    }
+    for (; k < gend; k += 256) {
 #pragma unroll
       for (int m = 0; m < G; ++m) mx[m] = fmaxf(mx[m], vsb[(int64_t)k * G + m]);
     }
@@ -255,14 +272,18 @@ void prefill_mfma_kernel(PrefillParams p) {
     for (int qt = 0; qt < 2; ++qt) {
       const int pos = q0 + 16 * qt + c16;
       const bool ok = active && pos < L;
-      const int64_t base = b * p.q.s[0] + (int64_t)head * p.q.s[1] + (int64_t)pos * p.q.s[2];
+      // every lane loads from a valid row (position clamped to L - 1) and masks afterwards: a load
+      // under `ok` became a branch with its own wait, 64 round trips in a row per wave
+      const int64_t base =
+          b * p.q.s[0] + (int64_t)head * p.q.s[1] + (int64_t)min(pos, L - 1) * p.q.s[2];
       float qv[4][8];
       float mx = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          qv[c][u] = ok ? bf16_bits_to_float(qbits[base + (32 * c + 8 * j4 + u) * p.q.s[3]]) : 0.0f;
+          const float x = bf16_bits_to_float(qbits[base + (32 * c + 8 * j4 + u) * p.q.s[3]]);
+          qv[c][u] = ok ? x : 0.0f;
           mx = fmaxf(mx, fabsf(qv[c][u]));
         }
       }
