@@ -694,6 +694,16 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
     }
   };
   if constexpr (!BC_REREAD) read_bc();
+  // x and z of every row converted before the first store: converted inside the row loop, a
+  // later row's conversion (a dtype branch) came after the earlier rows' stores, and the wait the
+  // compiler placed for its load there (vmcnt counts stores too) also waited for those stores
+  float xs[R], zs[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t pc = (uint32_t)min(row0 + r * SLOTS + slot, P - 1);
+    xs[r] = word_elem(L.xw[r], ((pc * p.x_row_bytes) & 2u) * 8u, p.x.dtype);
+    zs[r] = p.has_z ? word_elem(L.zw[r], ((pc * p.z_row_bytes) & 2u) * 8u, p.z.dtype) : 1.0f;
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if constexpr (BC_REREAD) {
@@ -703,7 +713,7 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
     const int pp = row0 + r * SLOTS + slot;
     const bool act = pp < P;
     const uint32_t pc = (uint32_t)min(pp, P - 1);
-    const float xv = word_elem(L.xw[r], ((pc * p.x_row_bytes) & 2u) * 8u, p.x.dtype);
+    const float xv = xs[r];
     // h' = h * exp(A dt) + (B dt) x, with the decay folded into the two pair scales (exact)
     const float s0 = pin(__uint_as_float(L.e[r] << 23) * hs.dA);
     const float s1 = pin(__uint_as_float((L.e[r] + 1u) << 23) * hs.dA);
@@ -722,7 +732,7 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
     for (int i = 0; i < 16; ++i) ypart = fmaf(hv[i], Cv[i], ypart);
     float y = row_sum<BPR_LOG2>(ypart);
     if (p.has_D) y += xv * hs.D;
-    if (p.has_z) y *= word_elem(L.zw[r], ((pc * p.z_row_bytes) & 2u) * 8u, p.z.dtype);
+    if (p.has_z) y *= zs[r];
     if (act && blk == 0) {
       const uint32_t oo = (uint32_t)pp * p.out_row_bytes;
       if (p.out.dtype == LQ_F32) {
