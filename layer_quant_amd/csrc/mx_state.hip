@@ -809,6 +809,19 @@ void mx_update_rows_kernel(MxUpdateParams p) {
   const int row0 = blockIdx.x * (R * SLOTS);
 
   const HeadBufs hb = head_bufs<N, LY>(p, b, h);
+  constexpr int CONV = (int)N / 2;  // converting threads (see below)
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  // The converting threads' B and C words are loaded before the state: every wave waits at the
+  // barrier for them, and issued after the state loads and the head scalars they came back one
+  // memory round trip after the state.
+  uint32_t bw = 0, cw = 0;
+  if (wave * 64 < CONV && (int)threadIdx.x < CONV) {
+    const int grp = h / p.ratio;
+    const auto rB = make_buf(vbase(p.B, b, grp), N * 2);
+    const auto rC = make_buf(vbase(p.C, b, grp), N * 2);
+    bw = __builtin_amdgcn_raw_buffer_load_b32(rB, 4u * threadIdx.x, 0, 0);
+    cw = __builtin_amdgcn_raw_buffer_load_b32(rC, 4u * threadIdx.x, 0, 0);
+  }
   RowLoads<R> L;
   load_rows<R, SLOTS, N, LY, RMODE>(p, hb, row0, slot, n0, L);
   // B * dt and C of the slice as fp32 and the head scalars, computed once per workgroup by the
@@ -817,18 +830,11 @@ void mx_update_rows_kernel(MxUpdateParams p) {
   // instructions per wave, the head scalars (softplus, exp) about 30 more. The same products as
   // before (B * dt rounded once), so the results are unchanged; at batch 64, MX4, one box: 40.9-41.1
   // -> 40.0-40.3 us, the arithmetic alone (timing-only copy) 36.8 -> 34.6 us.
-  constexpr int CONV = (int)N / 2;  // converting threads
   __shared__ float s_bd[N], s_c[N], s_hs[2];
-  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   if (wave * 64 < CONV) {  // wave-uniform
     const HeadScalars hs = head_scalars(p, b, h);
     if ((int)threadIdx.x < CONV) {
-      const int grp = h / p.ratio;
-      const auto rB = make_buf(vbase(p.B, b, grp), N * 2);
-      const auto rC = make_buf(vbase(p.C, b, grp), N * 2);
       const uint32_t t = threadIdx.x;
-      const uint32_t bw = __builtin_amdgcn_raw_buffer_load_b32(rB, 4u * t, 0, 0);
-      const uint32_t cw = __builtin_amdgcn_raw_buffer_load_b32(rC, 4u * t, 0, 0);
       s_bd[2 * t] = __uint_as_float(bw << 16) * hs.dt;
       s_bd[2 * t + 1] = __uint_as_float(bw & 0xffff0000u) * hs.dt;
       s_c[2 * t] = __uint_as_float(cw << 16);
