@@ -300,17 +300,22 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   const int64_t qbase = b * p.q.s[0] + (int64_t)(kvh * NREP + colh) * p.q.s[1];
   constexpr int kPerm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
   const bool use = colvalid && (q4 / CPG == colm);
+  // Every lane loads its 32 values (the address is valid for every lane) and the unused ones are
+  // zeroed afterwards: loaded under `use`, each pair became a branch with its own wait.
+  uint32_t qraw[4][8];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) qraw[c][k] = qbits[qbase + (32 * q4 + 8 * c + kPerm[k]) * p.q.s[2]];
+  }
   u32x4_t qop[4];
   float qsum = 0.0f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      uint32_t lo = 0, hi = 0;
-      if (use) {
-        lo = qbits[qbase + (32 * q4 + 8 * c + kPerm[2 * u]) * p.q.s[2]];
-        hi = qbits[qbase + (32 * q4 + 8 * c + kPerm[2 * u + 1]) * p.q.s[2]];
-      }
+      const uint32_t lo = use ? qraw[c][2 * u] : 0u;
+      const uint32_t hi = use ? qraw[c][2 * u + 1] : 0u;
       qsum += bf16_bits_to_float(lo) + bf16_bits_to_float(hi);
       qop[c][u] = lo | (hi << 16);
     }
