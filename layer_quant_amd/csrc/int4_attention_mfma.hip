@@ -341,10 +341,15 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
       pack_i = tile / WAVES;
       const int64_t kx = b * p.knew.s[0] + (int64_t)kvh * p.knew.s[1];
       const int64_t vx = b * p.vnew.s[0] + (int64_t)kvh * p.vnew.s[1];
-      kx0 = load_float(p.knew.data, p.knew.dtype, kx + 2 * lane * p.knew.s[2]);
-      kx1 = load_float(p.knew.data, p.knew.dtype, kx + (2 * lane + 1) * p.knew.s[2]);
-      vx0 = load_float(p.vnew.data, p.vnew.dtype, vx + 2 * lane * p.vnew.s[2]);
-      vx1 = load_float(p.vnew.data, p.vnew.dtype, vx + (2 * lane + 1) * p.vnew.s[2]);
+      uint32_t sh[4];
+      const uint32_t w0 = elem_word(p.knew.data, p.knew.dtype, kx + 2 * lane * p.knew.s[2], sh[0]);
+      const uint32_t w1 = elem_word(p.knew.data, p.knew.dtype, kx + (2 * lane + 1) * p.knew.s[2], sh[1]);
+      const uint32_t w2 = elem_word(p.vnew.data, p.vnew.dtype, vx + 2 * lane * p.vnew.s[2], sh[2]);
+      const uint32_t w3 = elem_word(p.vnew.data, p.vnew.dtype, vx + (2 * lane + 1) * p.vnew.s[2], sh[3]);
+      kx0 = word_elem(w0, sh[0], p.knew.dtype);
+      kx1 = word_elem(w1, sh[1], p.knew.dtype);
+      vx0 = word_elem(w2, sh[2], p.vnew.dtype);
+      vx1 = word_elem(w3, sh[3], p.vnew.dtype);
     }
   }
 

@@ -67,6 +67,26 @@ __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// Float value of the 16- or 32-bit element held in the 32-bit word w at bit `shift` (0 or 16).
+__device__ __forceinline__ float word_elem(uint32_t w, uint32_t shift, int dtype) {
+  const uint32_t h16 = (w >> shift) & 0xffffu;
+  if (dtype == LQ_F32) return __uint_as_float(w);
+  if (dtype == LQ_BF16) return __uint_as_float(h16 << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+// The aligned 32-bit word holding element idx of a bf16, fp16 or fp32 tensor, and the element's
+// bit offset in it (for word_elem). A 4-byte aligned word never crosses a page, so the read stays
+// inside the allocation's pages. Several such loads go out together and are converted after the
+// last; load_float's dtype branch waits after each load.
+__device__ __forceinline__ uint32_t elem_word(const void* base, int dtype, int64_t idx,
+                                              uint32_t& shift) {
+  const uintptr_t a = (uintptr_t)base + (uintptr_t)(idx * (dtype == LQ_F32 ? 4 : 2));
+  shift = (uint32_t)(a & 2u) * 8u;
+  typedef const __attribute__((address_space(1))) uint32_t* gword_t;  // a global load, not flat
+  return *(gword_t)(a & ~(uintptr_t)3);
+}
+
 __device__ __forceinline__ float load_float(const void* base, int dtype, int64_t idx) {
   switch (dtype) {
     case LQ_BF16:

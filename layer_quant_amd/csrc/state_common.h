@@ -90,14 +90,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* base, uin
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, BUF_DWORD3);
 }
 
-// Float value of the 16- or 32-bit element held in the 32-bit word w at bit `shift` (0 or 16).
-__device__ __forceinline__ float word_elem(uint32_t w, uint32_t shift, int dtype) {
-  const uint32_t h16 = (w >> shift) & 0xffffu;
-  if (dtype == LQ_F32) return __uint_as_float(w);
-  if (dtype == LQ_BF16) return __uint_as_float(h16 << 16);
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
-}
-
 // Element at a wave-uniform address, read by a scalar load of the aligned 32-bit word holding it
 // (a 4-byte aligned word never crosses a page, so it stays inside the allocation's pages).
 __device__ __forceinline__ uint32_t uniform_word(const char* addr) {
