@@ -644,14 +644,17 @@ bool fast_path_ok(const AttnParams& p) {
   return true;
 }
 
-// Waves of attn_fast_kernel resident on the current device at once: CUs x the workgroups per CU
-// that the occupancy calculator gives for the <4, 4> instance (its register and LDS use stand for
-// the others') x 4 waves.
-static int64_t resident_fast_waves() {
-  static int cached[64] = {0};
+// CUs of the current device and the workgroups per CU that the occupancy calculator gives for
+// the <4, 4> instance of attn_fast_kernel (its register and LDS use stand for the others').
+struct FastResidency {
+  int cus, per_cu;
+};
+
+static FastResidency fast_residency() {
+  static FastResidency cached[64] = {};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 2048;
-  if (cached[dev] == 0) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FastResidency{256, 2};
+  if (cached[dev].cus == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0) {
@@ -663,7 +666,7 @@ static int64_t resident_fast_waves() {
         per_cu <= 0) {
       per_cu = 2;
     }
-    cached[dev] = cus * per_cu * WAVES;
+    cached[dev] = FastResidency{cus, per_cu};
   }
   return cached[dev];
 }
@@ -673,10 +676,19 @@ SplitPlan plan_fast(int64_t B, int64_t Hkv, int64_t S) {
   // 32-key tile, 4 waves per workgroup split, the split's tiles dealt to the waves in turn).
   // Fewer, longer waves amortize the per-wave setup and the 4-wave merge, and at
   // B * Hkv >= resident / 4 no split-K merge runs at all.
-  const int64_t target_waves = resident_fast_waves();
+  const FastResidency r = fast_residency();
+  const int64_t target_waves = (int64_t)r.cus * r.per_cu * WAVES;
   int64_t tpw = (B * Hkv * S + target_waves - 1) / target_waves;
   tpw = ((tpw + TILE - 1) / TILE) * TILE;
   tpw = std::min<int64_t>(std::max<int64_t>(tpw, TILE), (int64_t)1 << 20);
+  // A wave of one or two tiles spends most of its time in set-up and the merges, so a wave takes
+  // at least 4 tiles while that still leaves a workgroup for every CU (batch 1, ctx 16384: 32
+  // splits instead of 64, 17.8 against 20.0 us; at ctx 1024 and 4096 4 tiles would leave 16 and
+  // 64 workgroups and ran slower, 15.8 and 16.8 against 13.7 and 14.2 us).
+  constexpr int64_t kMinTiles = 4 * TILE;
+  if (tpw < kMinTiles && B * Hkv * ((S + WAVES * kMinTiles - 1) / (WAVES * kMinTiles)) >= r.cus) {
+    tpw = kMinTiles;
+  }
   SplitPlan sp{};
   sp.chunk = WAVES * tpw;
   sp.nsplit = (int)std::max<int64_t>(1, (S + sp.chunk - 1) / sp.chunk);
