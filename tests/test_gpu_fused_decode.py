@@ -49,7 +49,7 @@ def _draw(n, seed):
     return out
 
 
-CASES = _draw(36, 4242)
+CASES = _draw(72, 4242)
 
 
 def _token(c, gen, gpu):

@@ -36,7 +36,7 @@ def _draw_cases(n, seed):
     return cases
 
 
-CASES = _draw_cases(40, 20241202)
+CASES = _draw_cases(100, 20241202)
 
 
 def _activations(shape, gen, outliers=True):

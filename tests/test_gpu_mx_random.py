@@ -51,7 +51,7 @@ def _draw_cases(n, seed):
     return cases
 
 
-CASES = _draw_cases(32, 1202)
+CASES = _draw_cases(96, 1202)
 
 
 @pytest.mark.parametrize("i,c", CASES, ids=[f"case{i}" for i, _ in CASES])

@@ -48,7 +48,7 @@ def _pack_cases(n, seed):
     return out
 
 
-PACK_CASES = _pack_cases(24, 77)
+PACK_CASES = _pack_cases(48, 77)
 
 
 @pytest.mark.parametrize("i,b,h,t,d,g,dt,pair", PACK_CASES, ids=[f"case{c[0]}" for c in PACK_CASES])
@@ -91,7 +91,7 @@ def _prefill_cases(n, seed):
     return out
 
 
-PREFILL_CASES = _prefill_cases(16, 88)
+PREFILL_CASES = _prefill_cases(32, 88)
 
 
 @pytest.mark.parametrize("i,b,hkv,nrep,L,g,qdt,odt", PREFILL_CASES,
@@ -142,7 +142,7 @@ def _ssm_cases(n, seed):
     return out
 
 
-SSM_CASES = _ssm_cases(16, 99)
+SSM_CASES = _ssm_cases(48, 99)
 
 
 @pytest.mark.parametrize("i,c", SSM_CASES, ids=[f"case{c[0]}" for c in SSM_CASES])
