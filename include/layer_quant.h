@@ -85,6 +85,33 @@ int lq_abi_version(void);
 const char* lq_last_error(void);
 
 /*
+ * Diagnostic switches, for tests and experiments (no counterpart in the reference). FORCE_*
+ * sends every call of a kernel family to its general kernel; REQUIRE_* makes a call that would
+ * take the general kernel fail with LQ_ERR_INVALID_ARG instead (a test's proof that a case runs
+ * the fast kernel). The library reads them once from the environment variables of the same
+ * names (set to anything but "" or "0") when it is loaded; afterwards only lq_set_diagnostics
+ * changes them. The switches are process-wide: set them between calls, not while another thread
+ * launches.
+ */
+enum {
+  LQ_DIAG_ATTN_FORCE_GENERIC = 1u << 0,
+  LQ_DIAG_ATTN_REQUIRE_FAST = 1u << 1,
+  LQ_DIAG_PREFILL_FORCE_GENERIC = 1u << 2,
+  LQ_DIAG_PREFILL_REQUIRE_MFMA = 1u << 3,
+  LQ_DIAG_MX_FORCE_GENERIC = 1u << 4,
+  LQ_DIAG_MX_REQUIRE_ROWS = 1u << 5,
+  LQ_DIAG_SSM_FORCE_GENERIC = 1u << 6,
+  LQ_DIAG_SSM_REQUIRE_ROWS = 1u << 7,
+  LQ_DIAG_ALL = (1u << 8) - 1
+};
+
+/* The current LQ_DIAG_* bits. */
+uint32_t lq_diagnostics(void);
+
+/* Replaces the LQ_DIAG_* bits (unknown bits are dropped); returns the previous ones. */
+uint32_t lq_set_diagnostics(uint32_t flags);
+
+/*
  * INT4 pack of new K or V tokens into the packed cache.
  * Replaces the launch of _pack_int4_kv_kernel (reference hybrid_quant/int4_8b_attention.py:32-111,
  * launched twice by _pack_kv_into_cache at :477-514).
@@ -168,7 +195,9 @@ int lq_int4_decode_attention_pack(const lq_tensor* q, const lq_tensor* k_new,
  * Every call on one GPU shares that GPU's buffer and it keeps the last call's partials (nothing
  * in it has to start at zero): calls that overlap on one GPU -- on different streams, or from
  * different host threads -- race and must be serialized by the caller; calls in order on one
- * stream are safe. The buffer is on the device that runs `stream`.
+ * stream are safe. The buffer is on the device that runs `stream`. The first call on a device
+ * resolves the buffer's device address (hipGetSymbolAddress); make that call outside any HIP
+ * graph capture (a warm-up call before capturing), after which captured calls only launch.
  */
 #define LQ_DECODE_ATTENTION_NOALLOC_SCRATCH_BYTES (8u << 20)
 int lq_int4_decode_attention_noalloc(const lq_tensor* q, const lq_tensor* k_packed,

@@ -7,6 +7,7 @@ the library must be built (python -m layer_quant_amd.build) and tensors must liv
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -27,6 +28,18 @@ ROUND_HALF_UP = 1
 ROUND_SR_UNIFORM = 2
 ROUND_SR_COUNTER = 3
 
+# LQ_DIAG_* bits of the library's diagnostic switches, by their environment-variable names
+DIAG_BITS = {
+    "LQ_ATTN_FORCE_GENERIC": 1 << 0,
+    "LQ_ATTN_REQUIRE_FAST": 1 << 1,
+    "LQ_PREFILL_FORCE_GENERIC": 1 << 2,
+    "LQ_PREFILL_REQUIRE_MFMA": 1 << 3,
+    "LQ_MX_FORCE_GENERIC": 1 << 4,
+    "LQ_MX_REQUIRE_ROWS": 1 << 5,
+    "LQ_SSM_FORCE_GENERIC": 1 << 6,
+    "LQ_SSM_REQUIRE_ROWS": 1 << 7,
+}
+
 DTYPE_CODES = {
     torch.uint8: 0,
     torch.int8: 1,
@@ -41,6 +54,8 @@ DTYPE_CODES = {
 EXPORTED_SYMBOLS = (
     "lq_abi_version",
     "lq_last_error",
+    "lq_diagnostics",
+    "lq_set_diagnostics",
     "lq_int4_pack_kv",
     "lq_int4_pack_kv_pair",
     "lq_int4_decode_attention_workspace",
@@ -83,6 +98,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.lq_abi_version.argtypes = []
     lib.lq_last_error.restype = ctypes.c_char_p
     lib.lq_last_error.argtypes = []
+    lib.lq_diagnostics.restype = ctypes.c_uint32
+    lib.lq_diagnostics.argtypes = []
+    lib.lq_set_diagnostics.restype = ctypes.c_uint32
+    lib.lq_set_diagnostics.argtypes = [ctypes.c_uint32]
     lib.lq_int4_pack_kv.restype = ctypes.c_int
     lib.lq_int4_pack_kv.argtypes = [_P, _P, _P, _P, ctypes.c_int, ctypes.c_void_p]
     lib.lq_int4_pack_kv_pair.restype = ctypes.c_int
@@ -185,6 +204,38 @@ def _stream(device: torch.device) -> int:
 
 def abi_version() -> int:
     return int(lib().lq_abi_version())
+
+
+def diagnostics() -> set[str]:
+    """Names of the diagnostic switches that are on (the library read them from the environment
+    when it was loaded; set_diagnostics changes them)."""
+    flags = int(lib().lq_diagnostics())
+    return {name for name, bit in DIAG_BITS.items() if flags & bit}
+
+
+def set_diagnostics(names) -> set[str]:
+    """Turn on exactly the switches in `names` (LQ_MX_REQUIRE_ROWS, ...); returns the previous
+    set. Process-wide: call it between kernel calls."""
+    flags = 0
+    for name in names:
+        if name not in DIAG_BITS:
+            raise ValueError(f"unknown diagnostic switch {name!r}")
+        flags |= DIAG_BITS[name]
+    prev = int(lib().lq_set_diagnostics(flags))
+    return {name for name, bit in DIAG_BITS.items() if prev & bit}
+
+
+@contextlib.contextmanager
+def diagnostic(*names: str, on: bool = True):
+    """Add the switches `names` for the block (nothing when `on` is false), then restore."""
+    if not on:
+        yield
+        return
+    prev = set_diagnostics(diagnostics() | set(names))
+    try:
+        yield
+    finally:
+        set_diagnostics(prev)
 
 
 def int4_pack_kv(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor,

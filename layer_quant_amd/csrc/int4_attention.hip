@@ -474,7 +474,7 @@ static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
   p.scale_sm = (float)(1.4426950408889634 / sqrt((double)D));
 
   const bool fast = fast_path_ok(p);
-  if (!fast && env_flag("LQ_ATTN_REQUIRE_FAST")) {  // tests: the call must take the MFMA kernel
+  if (!fast && diag(LQ_DIAG_ATTN_REQUIRE_FAST)) {  // tests: the call must take the MFMA kernel
     return fail(LQ_ERR_INVALID_ARG,
                 "LQ_ATTN_REQUIRE_FAST is set and this call takes the generic kernel");
   }

@@ -612,16 +612,8 @@ bool fast_path_shape_ok(int64_t head_dim, int group_size, int64_t n_q_heads,
   return nrep * (FAST_D / group_size) <= 16;
 }
 
-static bool force_generic() {
-  static const int v = [] {
-    const char* e = getenv("LQ_ATTN_FORCE_GENERIC");
-    return (e != nullptr && e[0] == '1') ? 1 : 0;
-  }();
-  return v != 0;
-}
-
 bool fast_path_ok(const AttnParams& p) {
-  if (force_generic()) return false;
+  if (diag(LQ_DIAG_ATTN_FORCE_GENERIC)) return false;
   if (!fast_path_shape_ok(p.D, p.g, p.Hq, p.Hkv)) return false;
   if (p.q.dtype != LQ_BF16) return false;
   // contiguous key rows: 64 packed bytes per key, D/g scale words per key

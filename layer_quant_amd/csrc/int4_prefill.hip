@@ -533,16 +533,8 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillParams p) {
   }
 }
 
-bool force_generic_prefill() {
-  static const int v = [] {
-    const char* e = getenv("LQ_PREFILL_FORCE_GENERIC");
-    return (e != nullptr && e[0] == '1') ? 1 : 0;
-  }();
-  return v != 0;
-}
-
 bool prefill_mfma_ok(const PrefillParams& p) {
-  if (force_generic_prefill()) return false;
+  if (diag(LQ_DIAG_PREFILL_FORCE_GENERIC)) return false;
   if (p.D != PD || (p.g != 32 && p.g != 64 && p.g != 128)) return false;
   if (p.q.dtype != LQ_BF16) return false;
   const int64_t G = PD / p.g;
@@ -646,7 +638,7 @@ extern "C" int lq_int4_prefill_attention(const lq_tensor* q, const lq_tensor* k_
 
   hipStream_t st = (hipStream_t)stream;
   const bool mfma = prefill_mfma_ok(p);
-  if (!mfma && env_flag("LQ_PREFILL_REQUIRE_MFMA")) {  // tests: the call must take the MFMA kernel
+  if (!mfma && diag(LQ_DIAG_PREFILL_REQUIRE_MFMA)) {  // tests: the call must take the MFMA kernel
     return fail(LQ_ERR_INVALID_ARG,
                 "LQ_PREFILL_REQUIRE_MFMA is set and this call takes the generic kernel");
   }

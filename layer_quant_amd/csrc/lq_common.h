@@ -39,11 +39,10 @@ inline bool is_float_dtype(int dtype) {
   return dtype == LQ_F32 || dtype == LQ_F16 || dtype == LQ_BF16;
 }
 
-// A diagnostic switch from the environment: set to anything but "" or "0".
-inline bool env_flag(const char* name) {
-  const char* v = getenv(name);
-  return v != nullptr && v[0] != '\0' && v[0] != '0';
-}
+// Diagnostic switches (LQ_DIAG_* bits): taken from the environment once, when the library is
+// loaded, and changed afterwards only by lq_set_diagnostics. Entry points read them with one
+// relaxed atomic load, so no launch path calls getenv.
+bool diag(uint32_t bit);
 
 // Validates pointer, rank and dtype of a descriptor; returns 0 or an LQ_ERR code (message set).
 int check_tensor(const lq_tensor* t, const char* name, int ndim, bool float_dtype,

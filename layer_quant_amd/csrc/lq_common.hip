@@ -2,6 +2,9 @@
 // descriptor validation.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
+
+#include <atomic>
 
 #include "lq_common.h"
 
@@ -61,6 +64,26 @@ int check_tensor(const lq_tensor* t, const char* name, int ndim, bool float_dtyp
   return LQ_OK;
 }
 
+// Environment names of the LQ_DIAG_* bits, in bit order.
+static const char* const kDiagEnv[] = {
+    "LQ_ATTN_FORCE_GENERIC", "LQ_ATTN_REQUIRE_FAST", "LQ_PREFILL_FORCE_GENERIC",
+    "LQ_PREFILL_REQUIRE_MFMA", "LQ_MX_FORCE_GENERIC", "LQ_MX_REQUIRE_ROWS",
+    "LQ_SSM_FORCE_GENERIC", "LQ_SSM_REQUIRE_ROWS"};
+
+static uint32_t diag_from_env() {
+  uint32_t flags = 0;
+  for (uint32_t i = 0; i < sizeof(kDiagEnv) / sizeof(kDiagEnv[0]); ++i) {
+    const char* v = getenv(kDiagEnv[i]);
+    if (v != nullptr && v[0] != '\0' && v[0] != '0') flags |= 1u << i;
+  }
+  return flags;
+}
+
+// initialised while the library loads (before any entry point can run)
+static std::atomic<uint32_t> g_diag{diag_from_env()};
+
+bool diag(uint32_t bit) { return (g_diag.load(std::memory_order_relaxed) & bit) != 0; }
+
 int64_t max_offset(const lq_tensor* t) {
   int64_t off = 0;
   for (int i = 0; i < t->ndim; ++i) {
@@ -75,3 +98,9 @@ int64_t max_offset(const lq_tensor* t) {
 extern "C" int lq_abi_version(void) { return LQ_ABI_VERSION; }
 
 extern "C" const char* lq_last_error(void) { return lq::g_last_error.c_str(); }
+
+extern "C" uint32_t lq_diagnostics(void) { return lq::g_diag.load(std::memory_order_relaxed); }
+
+extern "C" uint32_t lq_set_diagnostics(uint32_t flags) {
+  return lq::g_diag.exchange(flags & LQ_DIAG_ALL, std::memory_order_relaxed);
+}

@@ -1170,7 +1170,7 @@ static void dispatch_rows(const MxUpdateParams& p, int rmode, dim3 grid, hipStre
 static bool rows_path_ok(const MxUpdateParams& p, bool vec, bool bcvec, const lq_tensor* dt,
                          const lq_tensor* dt_bias, const lq_tensor* A, const lq_tensor* D,
                          int round_mode, int64_t total, int layout) {
-  if (env_flag("LQ_MX_FORCE_GENERIC")) return false;
+  if (diag(LQ_DIAG_MX_FORCE_GENERIC)) return false;
   if (!vec || !bcvec) return false;
   if (p.N != 64 && p.N != 128 && p.N != 256) return false;
   const int64_t q_row = layout == LAYOUT_CM4 ? p.N / 2 : p.N;
@@ -1350,7 +1350,7 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
     if (rc != LQ_OK) return rc;
     return check_launch("lq_mx_state_update");
   }
-  if (env_flag("LQ_MX_REQUIRE_ROWS")) {  // tests: the call must take the row kernel
+  if (diag(LQ_DIAG_MX_REQUIRE_ROWS)) {  // tests: the call must take the row kernel
     return fail(LQ_ERR_INVALID_ARG,
                 "LQ_MX_REQUIRE_ROWS is set and this call's layout takes the general kernel");
   }

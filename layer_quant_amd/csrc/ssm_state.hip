@@ -450,7 +450,7 @@ extern "C" int lq_selective_state_update(const lq_tensor* state, const lq_tensor
   };
   const bool bcvec = bcv(B) && bcv(C);
   hipStream_t s = (hipStream_t)stream;
-  const bool forced = env_flag("LQ_SSM_FORCE_GENERIC");
+  const bool forced = diag(LQ_DIAG_SSM_FORCE_GENERIC);
   const int64_t lim = (int64_t)1 << 28;
   const bool rows_ok =
       !forced && vec && bcvec && (N == 64 || N == 128 || N == 256) && state->stride[2] == N &&
@@ -488,7 +488,7 @@ extern "C" int lq_selective_state_update(const lq_tensor* state, const lq_tensor
     }
     return check_launch("lq_selective_state_update");
   }
-  if (env_flag("LQ_SSM_REQUIRE_ROWS")) {  // tests: the call must take the row kernel
+  if (diag(LQ_DIAG_SSM_REQUIRE_ROWS)) {  // tests: the call must take the row kernel
     return fail(LQ_ERR_INVALID_ARG,
                 "LQ_SSM_REQUIRE_ROWS is set and this call's layout takes the general kernel");
   }

@@ -178,7 +178,14 @@ def _pack_and_decode_attention(query_states: torch.Tensor, key_states: torch.Ten
         raise ValueError(f"Fused INT4 decode attention expects q_len=1, got {q_len}")
     out = torch.empty((batch, n_heads, head_dim), device=query_states.device,
                       dtype=query_states.dtype)
-    mask = _decode_attention_mask(attention_mask, batch, seq_len, query_states.device)
+    try:
+        mask = _decode_attention_mask(attention_mask, batch, seq_len, query_states.device)
+    except ValueError:
+        # the reference packs the token and moves cache.length before its mask check raises
+        # (ia.py:678 packs, :532 raises): leave the cache in that state on this error path too
+        _pack_kv_into_cache(cache, key_states, value_states,
+                            torch.tensor([seq_len - 1], device=key_states.device), group_size)
+        raise
     _abi.int4_decode_attention_pack(query_states, key_states, value_states, cache.k_packed,
                                     cache.v_packed, cache.k_scale, cache.v_scale, mask, out,
                                     seq_len, num_key_value_groups, group_size)

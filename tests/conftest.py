@@ -24,6 +24,27 @@ def gpu():
     return torch.device("cuda:0")
 
 
+@pytest.fixture
+def diag():
+    """The library's diagnostic switches for one test (LQ_MX_REQUIRE_ROWS, ...): .set(names)
+    turns switches on, .clear(names) off; the test's end restores the previous set."""
+    from layer_quant_amd import _abi
+
+    prev = _abi.diagnostics()
+
+    class Switches:
+        @staticmethod
+        def set(*names):
+            _abi.set_diagnostics(_abi.diagnostics() | set(names))
+
+        @staticmethod
+        def clear(*names):
+            _abi.set_diagnostics(_abi.diagnostics() - set(names))
+
+    yield Switches()
+    _abi.set_diagnostics(prev)
+
+
 def pytest_runtest_setup(item):
     if item.get_closest_marker("gpu") is not None:
         print(f"\n[gpu-test] {item.nodeid}", flush=True)

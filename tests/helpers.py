@@ -1,9 +1,6 @@
 """Shared checks of the test suite."""
 from __future__ import annotations
 
-import contextlib
-import os
-
 import numpy as np
 import torch
 
@@ -13,22 +10,13 @@ RTOL = 2e-3  # the attention output / updated state tolerance, fp32 accumulation
 REPORT: list[str] = []
 
 
-@contextlib.contextmanager
 def require_env(name: str, on: bool = True):
-    """Set the library's diagnostic switch `name` to 1 for the block (when `on`): with
-    LQ_ATTN_REQUIRE_FAST, LQ_PREFILL_REQUIRE_MFMA, LQ_MX_REQUIRE_ROWS or LQ_SSM_REQUIRE_ROWS set, a
+    """Turn the library's diagnostic switch `name` on for the block (when `on`): with
+    LQ_ATTN_REQUIRE_FAST, LQ_PREFILL_REQUIRE_MFMA, LQ_MX_REQUIRE_ROWS or LQ_SSM_REQUIRE_ROWS on, a
     call that would take the general kernel fails instead."""
-    prev = os.environ.get(name)
-    if on:
-        os.environ[name] = "1"
-    try:
-        yield
-    finally:
-        if on:
-            if prev is None:
-                del os.environ[name]
-            else:
-                os.environ[name] = prev
+    from layer_quant_amd import _abi
+
+    return _abi.diagnostic(name, on=on)
 
 
 def fast_attention_expected(q_dtype, head_dim: int, group_size: int, nrep: int) -> bool:

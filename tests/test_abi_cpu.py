@@ -34,6 +34,36 @@ def test_version_and_empty_error():
     assert isinstance(_abi.last_error(), str)
 
 
+def test_diagnostic_switches():
+    """The switches are set and read through the ABI; unknown bits are dropped; the context
+    manager restores the previous set. (That the library reads them from the environment at
+    load time is checked in a child process, whose library load sees a set variable.)"""
+    import subprocess
+    import sys
+
+    lib = _abi.lib()
+    prev = _abi.diagnostics()
+    try:
+        assert lib.lq_set_diagnostics(0xFFFFFFFF) == sum(_abi.DIAG_BITS[n] for n in prev)
+        assert lib.lq_diagnostics() == sum(_abi.DIAG_BITS.values())
+        _abi.set_diagnostics([])
+        with _abi.diagnostic("LQ_MX_REQUIRE_ROWS", "LQ_SSM_FORCE_GENERIC"):
+            assert _abi.diagnostics() == {"LQ_MX_REQUIRE_ROWS", "LQ_SSM_FORCE_GENERIC"}
+            with _abi.diagnostic("LQ_ATTN_REQUIRE_FAST", on=False):
+                assert "LQ_ATTN_REQUIRE_FAST" not in _abi.diagnostics()
+        assert _abi.diagnostics() == set()
+        with pytest.raises(ValueError):
+            _abi.set_diagnostics(["LQ_NOT_A_SWITCH"])
+    finally:
+        _abi.set_diagnostics(prev)
+    code = "from layer_quant_amd import _abi; print(sorted(_abi.diagnostics()))"
+    env = {k: v for k, v in __import__("os").environ.items() if not k.startswith("LQ_")}
+    env.update(LQ_PREFILL_REQUIRE_MFMA="1", LQ_MX_FORCE_GENERIC="0")
+    out = subprocess.run([sys.executable, "-c", code], env=env, cwd=ROOT, capture_output=True,
+                         text=True, check=True).stdout
+    assert out.strip() == "['LQ_PREFILL_REQUIRE_MFMA']"
+
+
 def _fake(shape, dtype, data=0x1000):
     """A descriptor with a non-null fake device address (never dereferenced by validation)."""
     t = _abi.LQTensor()

@@ -120,11 +120,11 @@ def _heads(t, n, d):
 
 
 @pytest.mark.parametrize("stochastic", [True, False])
-def test_driver_decode_loop(gpu, monkeypatch, stochastic):
+def test_driver_decode_loop(gpu, diag, stochastic):
     # every decode-step call of the patched model must take the library's fast kernels: the MFMA
     # attention, the MX row kernel and, for the unregistered layers, the unquantized row kernel
     for name in ("LQ_ATTN_REQUIRE_FAST", "LQ_MX_REQUIRE_ROWS", "LQ_SSM_REQUIRE_ROWS"):
-        monkeypatch.setenv(name, "1")
+        diag.set(name)
     fk.reset_module()
     torch.manual_seed(0)
     cfg = fk.make_config(hybrid_override_pattern="M*M-M*M", num_attention_heads=8,

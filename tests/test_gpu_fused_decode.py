@@ -72,7 +72,7 @@ def _mask(kind, b, s, gen):
 
 
 @pytest.mark.parametrize("c", CASES, ids=[f"case{c['i']}" for c in CASES])
-def test_fused_pack_attention_equals_two_calls(gpu, monkeypatch, c):
+def test_fused_pack_attention_equals_two_calls(gpu, diag, c):
     print(f"[fused case {c['i']}] {c}", flush=True)
     b, hkv, nrep, s, g = c["b"], c["hkv"], c["nrep"], c["s"], c["g"]
     gen = torch.Generator().manual_seed(7000 + c["i"])
@@ -89,7 +89,7 @@ def test_fused_pack_attention_equals_two_calls(gpu, monkeypatch, c):
     mask = _mask(c["mask"], b, s, gen)
     mask = None if mask is None else mask.to(gpu)
     if fast_attention_expected(q.dtype, D, g, nrep):  # then the fused MFMA kernel is required
-        monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
+        diag.set("LQ_ATTN_REQUIRE_FAST")
     sep = [t.clone() for t in (kp, vp, ks, vs)]
     fus = [t.clone() for t in (kp, vp, ks, vs)]
     out_sep = torch.full((b, hkv * nrep, D), float("nan"), dtype=DTYPES[c["odt"]], device=gpu)
@@ -142,3 +142,31 @@ def test_fused_repeats_bit_identical(gpu, b, s, g):
             assert torch.equal(out, ref)
     assert all(torch.equal(a, f) for a, f in zip(first, (kp, vp, ks, vs)))
     assert torch.isfinite(ref).all()
+
+
+def test_fused_branch_bad_mask_leaves_token_packed(gpu):
+    """A mask of unsupported rank raises ValueError after the token is packed and cache.length
+    moved, as in the reference, whose decode branch packs (ia.py:678) before its mask check
+    raises (:532)."""
+    from hybrid_quant import int4_8b_attention as ia
+
+    b, hkv, nrep, g, s = 2, 8, 4, 32, 40
+    gen = torch.Generator().manual_seed(5)
+    holder = type("Cache", (), {})()
+    cache = ia._ensure_layer_cache(holder, 0, b, hkv, s, D, g, gpu)
+    cache.k_packed.zero_(), cache.v_packed.zero_(), cache.k_scale.zero_(), cache.v_scale.zero_()
+    cache.length = s - 1
+    q = torch.randn(b, hkv * nrep, 1, D, generator=gen).to(torch.bfloat16).to(gpu)
+    kn = torch.randn(b, hkv, 1, D, generator=gen).to(torch.bfloat16).to(gpu)
+    vn = torch.randn(b, hkv, 1, D, generator=gen).to(torch.bfloat16).to(gpu)
+    bad_mask = torch.ones(b, 1, s, device=gpu)
+    with pytest.raises(ValueError, match="2D or 4D"):
+        ia._pack_and_decode_attention(q, kn, vn, cache, s, nrep, g, attention_mask=bad_mask)
+    assert cache.length == s
+    for x, pk, sc in ((kn, cache.k_packed, cache.k_scale), (vn, cache.v_packed, cache.v_scale)):
+        rp = torch.zeros(b, hkv, 1, D // 2, dtype=torch.uint8)
+        rs = torch.zeros(b, hkv, 1, D // g)
+        oik.pack_into(rp, rs, x.cpu(), torch.tensor([0]), g)
+        assert torch.equal(pk[:, :, s - 1:s].cpu(), rp)
+        assert torch.equal(sc[:, :, s - 1:s].cpu(), rs)
+        assert not pk[:, :, : s - 1].any()

@@ -1,7 +1,9 @@
 """A decode step captured in a HIP graph (through torch.cuda.CUDAGraph): the attention layer as
-the fused K+V pack and the decode attention, or as the one call that packs and attends
-(lq_int4_decode_attention_pack), with split-K partials in the per-stream workspace, and an MX4
-state update with the counter generator. Three replays, with eager GPU work and synchronizations between them, each
+the fused K+V pack and the decode attention, as the one call that packs and attends
+(lq_int4_decode_attention_pack), both with split-K partials in the per-stream workspace, or as
+the K+V pack and lq_int4_decode_attention_noalloc (partials in the library's static scratch; its
+first call on the device, which resolves the scratch address, is the warm-up before the
+capture), and an MX4 state update with the counter generator. Three replays, with eager GPU work and synchronizations between them, each
 match the same calls run eagerly, bit for bit. None of these entry points records a memset."""
 import pytest
 import torch
@@ -49,7 +51,12 @@ def _make_state(gpu, seed):
 
 def _step(t):
     s, nrep, g = t["dims"]
-    if t["fused"]:
+    if t["mode"] == "noalloc":
+        _abi.int4_pack_kv_pair(t["k_new"], t["v_new"], t["kp"], t["vp"], t["ks"], t["vs"],
+                               t["pos"], g)
+        _abi.int4_decode_attention_noalloc(t["q"], t["kp"], t["vp"], t["ks"], t["vs"], None,
+                                           t["att"], s, nrep, g)
+    elif t["mode"] == "fused":
         _abi.int4_decode_attention_pack(t["q"], t["k_new"], t["v_new"], t["kp"], t["vp"], t["ks"],
                                         t["vs"], None, t["att"], s, nrep, g)
     else:
@@ -70,10 +77,14 @@ def _restore(t, snap):
         dst.copy_(src)
 
 
-@pytest.mark.parametrize("fused", [False, True], ids=["pack+attention", "fused"])
-def test_decode_step_graph_replays_match_eager(gpu, fused):
+@pytest.mark.parametrize("mode", ["pack+attention", "fused", "noalloc"])
+def test_decode_step_graph_replays_match_eager(gpu, mode):
     t = _make_state(gpu, 2024)
-    t["fused"] = fused
+    t["mode"] = mode
+    s, nrep, g = t["dims"]
+    b, hkv, _, half_d = t["kp"].shape
+    # several key splits, so that the partials (workspace or static scratch) are used
+    assert _abi.lib().lq_int4_decode_attention_workspace(b, hkv * nrep, hkv, 2 * half_d, s, g) > 0
     start = _snapshot(t)
     eager = []
     for _ in range(3):  # the state update feeds the next step's state

@@ -251,11 +251,11 @@ def test_attention_long_wave_ranges_masked(gpu, s, g):
                                                    (2, 2, 16, 777, 128, False),
                                                    (64, 8, 4, 1057, 64, True),
                                                    (8, 8, 4, 4133, 32, True)])
-def test_attention_repeats_bit_identical(gpu, monkeypatch, b, hkv, nrep, s, g, masked):
+def test_attention_repeats_bit_identical(gpu, diag, b, hkv, nrep, s, g, masked):
     """The MFMA path's tile loads land in LDS behind explicit waits: repeated calls on the same
     inputs must give bit-identical outputs (a missing or short wait would read a tile early).
     The masked instance counts 7 loads per tile in its waits."""
-    monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
+    diag.set("LQ_ATTN_REQUIRE_FAST")
     d = 128
     gen = torch.Generator(device=gpu).manual_seed(b * 7 + s)
     kp = torch.randint(0, 256, (b, hkv, s, d // 2), dtype=torch.uint8, device=gpu, generator=gen)
@@ -278,10 +278,10 @@ def test_attention_repeats_bit_identical(gpu, monkeypatch, b, hkv, nrep, s, g, m
     assert torch.isfinite(ref).all()
 
 
-def test_attention_concurrent_streams(gpu, monkeypatch):
+def test_attention_concurrent_streams(gpu, diag):
     """Split-K calls in flight on two streams at once use separate workspaces (one per stream):
     each stream's results equal the same calls made one at a time on the default stream."""
-    monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
+    diag.set("LQ_ATTN_REQUIRE_FAST")
     b, hkv, nrep, d, g = 2, 8, 4, 128, 32
     cases = []
     for i, s in enumerate((3000, 1777)):
@@ -311,9 +311,9 @@ def test_attention_concurrent_streams(gpu, monkeypatch):
 
 
 @pytest.mark.parametrize("b,s", [(64, 16384), (8, 4096)])
-def test_attention_full_size_sampled_heads(gpu, monkeypatch, b, s):
+def test_attention_full_size_sampled_heads(gpu, diag, b, s):
     """BASELINE sizes: random packed cache built on the GPU, oracle on sampled (b, kv head)."""
-    monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
+    diag.set("LQ_ATTN_REQUIRE_FAST")
     hkv, nrep, d, g = 8, 4, 128, 32
     gen = torch.Generator(device=gpu).manual_seed(b + s)
     kp = torch.randint(0, 256, (b, hkv, s, d // 2), dtype=torch.uint8, device=gpu, generator=gen)

@@ -26,10 +26,10 @@ HKV, NREP, D = 8, 4, 128
 
 
 @pytest.fixture(autouse=True)
-def _mfma_kernel_required(monkeypatch):
+def _mfma_kernel_required(diag):
     """Every call here (bf16 queries, 4 query heads per KV head, group 32/64/128) must take the
     MFMA kernel: the library refuses it otherwise."""
-    monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
+    diag.set("LQ_ATTN_REQUIRE_FAST")
 
 
 def _outlier_channels(gen, device, hkv=HKV, d=D, frac=0.01):

@@ -65,7 +65,7 @@ def _mask(kind, b, s, gen):
 
 @pytest.mark.parametrize("i,b,hkv,nrep,s,g,mask_kind,qdt", CASES,
                          ids=[f"case{c[0]}" for c in CASES])
-def test_attention_random_shapes(gpu, monkeypatch, i, b, hkv, nrep, s, g, mask_kind, qdt):
+def test_attention_random_shapes(gpu, diag, i, b, hkv, nrep, s, g, mask_kind, qdt):
     print(f"[case {i}] b={b} hkv={hkv} nrep={nrep} s={s} g={g} mask={mask_kind} q={qdt}",
           flush=True)
     gen = torch.Generator().manual_seed(1000 + i)
@@ -78,7 +78,7 @@ def test_attention_random_shapes(gpu, monkeypatch, i, b, hkv, nrep, s, g, mask_k
     if qdt == "f32":
         q = q.float()
     if fast_attention_expected(q.dtype, D, g, nrep):  # then the MFMA kernel is required
-        monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
+        diag.set("LQ_ATTN_REQUIRE_FAST")
     mask = _mask(mask_kind, b, s, gen)
     ref = oik.decode_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
                                cache["v_scale"], s, nrep, g, mask=mask)

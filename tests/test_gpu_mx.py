@@ -91,13 +91,13 @@ def _inputs(bsz, nh, p_, n, ng, seed, device, dt_zero=False, head_dt=False):
 
 
 @pytest.fixture(params=["rows", "general"])
-def path(request, monkeypatch):
+def path(request, diag):
     """Run a test on the row kernel's layout (the library refuses the call if it would take the
     general kernel), and once more with the general kernel forced."""
     if request.param == "general":
-        monkeypatch.setenv("LQ_MX_FORCE_GENERIC", "1")
+        diag.set("LQ_MX_FORCE_GENERIC")
     else:
-        monkeypatch.setenv("LQ_MX_REQUIRE_ROWS", "1")
+        diag.set("LQ_MX_REQUIRE_ROWS")
     return request.param
 
 
@@ -130,10 +130,10 @@ def test_update_dt_zero_writeback_bit_exact(gpu, path, fb, mode):
 @pytest.mark.parametrize("fb", [8, 4])
 @pytest.mark.parametrize("softplus", [True, False])
 @pytest.mark.parametrize("head_dt", [True, False])
-def test_update_parity(gpu, monkeypatch, fb, softplus, head_dt):
+def test_update_parity(gpu, diag, fb, softplus, head_dt):
     bsz, nh, p_, n, ng = 4, 32, 16, 128, 4
     if head_dt:  # the model's layout: the row kernel
-        monkeypatch.setenv("LQ_MX_REQUIRE_ROWS", "1")
+        diag.set("LQ_MX_REQUIRE_ROWS")
     shape = (bsz, nh, p_, n)
     h0 = _state(shape, 40 + fb)
     q, e, m = omx.mx_encode(h0.numpy(), fb, 0)
@@ -186,13 +186,13 @@ def test_update_general_A_and_strides(gpu):
 
 @pytest.mark.parametrize("fb", [8, 4])
 @pytest.mark.parametrize("n", [64, 96, 128, 256])
-def test_update_counter_mode_nonzero_dt(gpu, path, monkeypatch, fb, n):
+def test_update_counter_mode_nonzero_dt(gpu, path, diag, fb, n):
     """Counter-mode writeback after a real update on the row kernel's layout (d_state 64, 128,
     256, and 96 on the general kernel): y within 2e-3, the state equal to the oracle's except
     at encoder decision ties (one level at most); P = 40 leaves a partly filled last row
     group."""
     if n == 96:
-        monkeypatch.delenv("LQ_MX_REQUIRE_ROWS", raising=False)
+        diag.clear("LQ_MX_REQUIRE_ROWS")
     bsz, nh, p_, ng = 2, 8, 40, 2
     shape = (bsz, nh, p_, n)
     h0 = _state(shape, 90 + fb + n)

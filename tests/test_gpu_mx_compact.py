@@ -41,13 +41,13 @@ def _as_np(t):
 
 
 @pytest.fixture(params=["rows", "general"])
-def path(request, monkeypatch):
+def path(request, diag):
     """The row kernel (required: the library refuses a call that would take the general
     kernel), then the general kernel forced."""
     if request.param == "general":
-        monkeypatch.setenv("LQ_MX_FORCE_GENERIC", "1")
+        diag.set("LQ_MX_FORCE_GENERIC")
     else:
-        monkeypatch.setenv("LQ_MX_REQUIRE_ROWS", "1")
+        diag.set("LQ_MX_REQUIRE_ROWS")
     return request.param
 
 
@@ -138,10 +138,10 @@ def test_module_api_compact_chain_and_conversion(gpu, fb):
     assert torch.equal(ms.dequantize_state_cache(cmp_), ms.dequantize_state_cache(ref))
 
 
-def test_full_size_b64_compact_mx4(gpu, monkeypatch):
+def test_full_size_b64_compact_mx4(gpu, diag):
     """Nemotron-H layer at batch 64 in the compact MX4 layout (row kernel), one counter-mode
     step: bit-identical to the reference layout."""
-    monkeypatch.setenv("LQ_MX_REQUIRE_ROWS", "1")
+    diag.set("LQ_MX_REQUIRE_ROWS")
     bsz, nh, p_, n, ng = 64, 128, 64, 128, 8
     g = torch.Generator(device=gpu).manual_seed(8)
     h0 = torch.randn(bsz, nh, p_, n, device=gpu, generator=g) * 0.5

@@ -55,13 +55,13 @@ CASES = _draw_cases(96, 1202)
 
 
 @pytest.mark.parametrize("i,c", CASES, ids=[f"case{i}" for i, _ in CASES])
-def test_mx_update_random(gpu, monkeypatch, i, c):
+def test_mx_update_random(gpu, diag, i, c):
     # the row kernel's layout: dt and A constant along head_dim, d_state 64/128/256, and in
     # counter mode an offset that is a multiple of 16; the library must then take that kernel
     rows = (c["head_dt"] and not c["a_rows"] and c["n"] != 96
             and not (c["mode"] == 3 and c["off"] % 16 != 0))
     if rows:
-        monkeypatch.setenv("LQ_MX_REQUIRE_ROWS", "1")
+        diag.set("LQ_MX_REQUIRE_ROWS")
     print(f"[case {i}] {'rows' if rows else 'general'} {c}", flush=True)
     g = torch.Generator().manual_seed(5000 + i)
     bsz, nh, p_, n, ng = c["bsz"], c["ng"] * c["ratio"], c["p"], c["n"], c["ng"]

@@ -76,10 +76,10 @@ def test_prefill_generic_shapes(gpu, b, hkv, nrep, L, g, d):
     assert_close_rel(_run(gpu, cache, q, nrep, g), _oracle(cache, q, nrep, g))
 
 
-def test_prefill_strided_query_and_module_api(gpu, monkeypatch):
+def test_prefill_strided_query_and_module_api(gpu, diag):
     """The model's query_states is a transposed view [B, L, Hq, D] -> [B, Hq, L, D], taken by the
     MFMA kernel; _prefill_attention returns q's dtype like the reference (ia.py:600)."""
-    monkeypatch.setenv("LQ_PREFILL_REQUIRE_MFMA", "1")
+    diag.set("LQ_PREFILL_REQUIRE_MFMA")
     b, hkv, nrep, L, d, g = 2, 2, 4, 77, 128, 32
     cache = _packed_cache(b, hkv, L, d, g, 980, cap=128)
     q_bl = _activations((b, L, hkv * nrep, d), 981).transpose(1, 2)
@@ -90,12 +90,12 @@ def test_prefill_strided_query_and_module_api(gpu, monkeypatch):
     assert_close_rel(out.float().cpu(), _oracle(cache, q_bl.contiguous(), nrep, g), rtol=8e-3)
 
 
-def test_prefill_full_size_sampled_rows(gpu, monkeypatch):
+def test_prefill_full_size_sampled_rows(gpu, diag):
     """Nemotron-H attention layer at L = 16384 (32 q heads, 8 KV heads, group 32): sampled
     (head, position) rows against the oracle's decode over the row's prefix, and the last row
     against the HIP decode kernel over the whole cache (both calls on their MFMA kernels)."""
-    monkeypatch.setenv("LQ_PREFILL_REQUIRE_MFMA", "1")
-    monkeypatch.setenv("LQ_ATTN_REQUIRE_FAST", "1")
+    diag.set("LQ_PREFILL_REQUIRE_MFMA")
+    diag.set("LQ_ATTN_REQUIRE_FAST")
     b, hkv, nrep, L, d, g = 1, 8, 4, 16384, 128, 32
     gen = torch.Generator(device=gpu).manual_seed(16384)
     kp = torch.randint(0, 256, (b, hkv, L, d // 2), dtype=torch.uint8, device=gpu, generator=gen)

@@ -96,7 +96,7 @@ PREFILL_CASES = _prefill_cases(32, 88)
 
 @pytest.mark.parametrize("i,b,hkv,nrep,L,g,qdt,odt", PREFILL_CASES,
                          ids=[f"case{c[0]}" for c in PREFILL_CASES])
-def test_prefill_random(gpu, monkeypatch, i, b, hkv, nrep, L, g, qdt, odt):
+def test_prefill_random(gpu, diag, i, b, hkv, nrep, L, g, qdt, odt):
     print(f"[prefill case {i}] b={b} hkv={hkv} nrep={nrep} L={L} g={g} q={qdt} out={odt}",
           flush=True)
     d = 128
@@ -110,7 +110,7 @@ def test_prefill_random(gpu, monkeypatch, i, b, hkv, nrep, L, g, qdt, odt):
     if qdt == "f32":
         q = q.float()
     if prefill_mfma_expected(q.dtype, d, g):  # then the MFMA kernel is required
-        monkeypatch.setenv("LQ_PREFILL_REQUIRE_MFMA", "1")
+        diag.set("LQ_PREFILL_REQUIRE_MFMA")
     ref = oik.prefill_attention(q, cache["k_packed"], cache["v_packed"], cache["k_scale"],
                                 cache["v_scale"], nrep, g)
     dev = {n_: t.to(gpu) for n_, t in cache.items() if torch.is_tensor(t)}
@@ -146,10 +146,10 @@ SSM_CASES = _ssm_cases(48, 99)
 
 
 @pytest.mark.parametrize("i,c", SSM_CASES, ids=[f"case{c[0]}" for c in SSM_CASES])
-def test_unquantized_update_random(gpu, monkeypatch, i, c):
+def test_unquantized_update_random(gpu, diag, i, c):
     rows = c["head_const"] and c["n"] != 96  # the row kernel's layout: required to take it
     if rows:
-        monkeypatch.setenv("LQ_SSM_REQUIRE_ROWS", "1")
+        diag.set("LQ_SSM_REQUIRE_ROWS")
     print(f"[ssm case {i}] {'rows' if rows else 'general'} {c}", flush=True)
     g = torch.Generator().manual_seed(600 + i)
     bsz, ng, n, p_ = c["bsz"], c["ng"], c["n"], c["p"]

@@ -41,13 +41,13 @@ def _inputs(bsz, nh, p_, n, ng, seed, head_const=True, z=False, dt_zero=False):
 
 
 @pytest.fixture(params=["rows", "general"])
-def path(request, monkeypatch):
+def path(request, diag):
     """Run a model-layout test on the row kernel (the library refuses a call that would take the
     general kernel), and once more with the general kernel forced."""
     if request.param == "general":
-        monkeypatch.setenv("LQ_SSM_FORCE_GENERIC", "1")
+        diag.set("LQ_SSM_FORCE_GENERIC")
     else:
-        monkeypatch.setenv("LQ_SSM_REQUIRE_ROWS", "1")
+        diag.set("LQ_SSM_REQUIRE_ROWS")
     return request.param
 
 

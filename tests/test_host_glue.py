@@ -222,3 +222,43 @@ def test_load_wikitext_texts_filters_blank_lines(monkeypatch, tmp_path):
     assert data.load_wikitext_texts(str(tmp_path), split="validation") == ["a", " b "]
     assert calls == [("wikitext", "wikitext-103-raw-v1", "test"),
                      (str(tmp_path), "wikitext-103-raw-v1", "validation")]
+
+
+def test_token_segments_window_boundaries():
+    """token_segments (reference data.py:23-32): windows of up to context_length + 1 tokens
+    starting every context_length tokens, sharing one token with the next window, over the
+    first min(n - 1, max_eval_tokens) predicted tokens of the texts joined by blank lines."""
+    from types import SimpleNamespace
+
+
+    from hybrid_quant import data
+
+    seen = []
+
+    def tokenizer(text, add_special_tokens, return_tensors):
+        seen.append((text, add_special_tokens, return_tensors))
+        return SimpleNamespace(input_ids=torch.arange(len(text)).unsqueeze(0))
+
+    def windows(n, ctx, cap):
+        seen.clear()
+        out = [w.tolist() for w in data.token_segments(tokenizer, ["x" * (n - 2), ""], ctx, cap)]
+        assert seen == [("x" * (n - 2) + "\n\n", False, "pt")]
+        return out
+
+    r = list(range(11))
+    # 11 tokens, 10 predicted: starts 0, 4, 8; the last window is short
+    assert windows(11, 4, 100) == [r[0:5], r[4:9], r[8:11]]
+    # max_eval_tokens caps the predicted tokens at 6: the last window ends at token 6
+    assert windows(11, 4, 6) == [r[0:5], r[4:7]]
+    # an exact multiple: 8 predicted tokens in two full windows
+    assert windows(9, 4, 100) == [r[0:5], r[4:9]]
+    # one token per window (context 1): every window is an (input, target) pair
+    assert windows(4, 1, 100) == [[0, 1], [1, 2], [2, 3]]
+    # two tokens: one window; nothing to predict with fewer
+    assert windows(2, 4, 100) == [[0, 1]]
+    assert windows(2, 4, 0) == []
+    with pytest.raises(ValueError):
+        next(data.token_segments(tokenizer, ["abc"], 0, 10))
+    # every predicted token is the target of exactly one window
+    targets = [t for w in windows(50, 7, 40) for t in w[1:]]
+    assert targets == list(range(1, 41))
