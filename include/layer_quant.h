@@ -58,15 +58,18 @@ enum {
   LQ_ROUND_NEAREST_EVEN = 0, /* torch.round of clamp(|v|/scale, 0, M): the initial encode       */
   LQ_ROUND_HALF_UP = 1,      /* floor(min(|v|/scale, M) + 0.5): the deterministic writeback     */
   LQ_ROUND_SR_UNIFORM = 2,   /* floor(q) + (u < q - floor(q)), u from a caller fp32 tensor       */
-  LQ_ROUND_SR_COUNTER = 3    /* same comparison, u from the library's counter-based generator    */
+  LQ_ROUND_SR_COUNTER = 3    /* stochastic, 16-bit draws of the library's counter generator:    */
+                             /* floor(RN_{2^-16}(v/scale + u)), u = u16 * 2^-16 (see below)     */
 };
 /*
  * The counter-based generator of LQ_ROUND_SR_COUNTER: element (b,h,p,n) draws counter
  * c = rng_offset + ((b*H + h)*P + p)*N + n (the reference's tl.rand offsets, step*B*H*P*N + index,
  * when rng_offset = step*B*H*P*N). With K = lowbias32(lo32(seed) ^ lowbias32(hi32(seed) ^
  * 0x9E3779B9)) and W = lowbias32(lo32(c>>1) ^ lowbias32(hi32(c>>1) ^ K)), the draw is
- * u16 = (W >> 16*(c&1)) & 0xFFFF, and the level is (trunc(v * 2^16 / pair_scale) + u16) >> 16 (a
- * fixed-point dither that rounds up with probability floor(frac * 2^16) / 2^16).
+ * u16 = (W >> 16*(c&1)) & 0xFFFF. With qs = v / pair_scale (exact) the level is
+ * floor(t) - 192, t = fp32(192 + u16 * 2^-16 + qs) clamped to [192 - M, 193 + M - 2^-16]: qs plus
+ * the draw rounded to the 2^-16 grid (ties to even), floored, so |v| rounds up with probability
+ * round(frac(|qs|) * 2^16) / 2^16 (bias within 2^-17 of a level step).
  * lowbias32(x): x ^= x>>16; x *= 0x7feb352d; x ^= x>>15; x *= 0x846ca68b; x ^= x>>16.
  */
 

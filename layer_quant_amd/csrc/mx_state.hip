@@ -21,8 +21,8 @@
 //   base = absmax == 0 ? 1 : 2^(e-127);  micro = pair_absmax > M*base
 //   qa = min(|v| / (base*2^micro), M)        as a product with the exact reciprocal
 //   level = rint(qa) | floor(qa + 0.5) | floor(qa) + (u < qa - floor(qa))   (always <= M)
-// The counter mode (LQ_ROUND_SR_COUNTER) draws 16-bit integers u16 and dithers in fixed point:
-//   T = trunc(clamp(v * 2^16 / (base*2^micro), -M*2^16, M*2^16)),  level = (T + u16) >> 16
+// The counter mode (LQ_ROUND_SR_COUNTER) draws 16-bit integers u16 and dithers on a 2^-16 grid:
+//   t = RN(v / (base*2^micro) + 192 + u16 * 2^-16)  (one fma),  level = floor(t) - 192
 #include <math.h>
 #include <stdlib.h>
 
@@ -103,11 +103,19 @@ __device__ __forceinline__ uint32_t micro(const uint32_t (&mw)[2], int k) {
   }
 }
 
-// Level bytes qw[4] (one int8 per value) and micro flags mb[8] (0/1) of an encoded block, in the
+// A constant held in an SGPR: a select between 0 and it is one v_cndmask_b32 (the compiler
+// otherwise materialises each shifted flag constant in a VGPR with a v_mov first).
+__device__ __forceinline__ uint32_t sgpr_const(uint32_t c) {
+  uint32_t r;
+  asm("s_mov_b32 %0, %1" : "=s"(r) : "i"(c));
+  return r;
+}
+
+// Level bytes qw[4] (one int8 per value) and micro flags mi[8] of an encoded block, in the
 // layout's raw form: nibbles qw[0..1] and micro bits mw[0] for the compact layouts.
 template <int LY>
 __device__ __forceinline__ void pack_block(uint32_t (&qw)[4], uint32_t (&mw)[2],
-                                           const uint32_t (&mb)[8]) {
+                                           const bool (&mi)[8]) {
   if constexpr (LayoutOf<LY>::qnib) {
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
@@ -121,12 +129,16 @@ __device__ __forceinline__ void pack_block(uint32_t (&qw)[4], uint32_t (&mw)[2],
   if constexpr (LayoutOf<LY>::mbits) {
     uint32_t bits = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) bits |= mb[k] << k;
+    for (int k = 0; k < 8; ++k) bits |= mi[k] ? (k == 7 ? sgpr_const(0x80u) : 1u << k) : 0u;
     mw[0] = bits;
     mw[1] = 0;
   } else {
-    mw[0] = mb[0] | (mb[1] << 8) | (mb[2] << 16) | (mb[3] << 24);
-    mw[1] = mb[4] | (mb[5] << 8) | (mb[6] << 16) | (mb[7] << 24);
+    const uint32_t b1 = sgpr_const(0x100u), b2 = sgpr_const(0x10000u), b3 = sgpr_const(0x1000000u);
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      mw[w] = (mi[4 * w] ? 1u : 0u) | (mi[4 * w + 1] ? b1 : 0u) | (mi[4 * w + 2] ? b2 : 0u) |
+              (mi[4 * w + 3] ? b3 : 0u);
+    }
   }
 }
 
@@ -279,6 +291,13 @@ __device__ __forceinline__ float pair_maxima(const float (&v)[16], float (&pa)[8
   return max_with_zero(max3(m, pa[5], pa[6]), pa[7]);
 }
 
+// Exact reciprocal of the pair scale 2^(se-127): normal for se <= 253, the subnormal 2^-127 for
+// se = 254, and 0 for se = 255 (scale +inf; only reachable when absmax is +inf, as |v| / inf is 0).
+__device__ __forceinline__ float pair_recip(int se) {
+  return se <= 253 ? __uint_as_float((uint32_t)(254 - se) << 23)
+                   : (se == 254 ? __uint_as_float(0x00400000u) : 0.0f);
+}
+
 // Encode 16 values in the nearest-even, half-up or supplied-uniform mode. `u16` holds the
 // supplied uniforms scaled by 2^16 (so that the comparison u < frac becomes u16 < frac * 2^16,
 // both sides exact), unused otherwise. The reference's final min(level, M) is omitted: every mode
@@ -293,17 +312,11 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16
   int eb, ebase;
   block_exponent_fast<FB>(amax, eb, ebase);
   const float thr = M * __uint_as_float((uint32_t)ebase << 23);
-  // exact reciprocals of the pair scales 2^(se-127), se = ebase + micro: normal for se <= 253,
-  // the subnormal 2^-127 for se = 254, and 0 for se = 255 (scale +inf; only reachable when
-  // absmax is +inf, as |v| / inf is 0)
-  auto recip = [](int se) {
-    return se <= 253 ? __uint_as_float((uint32_t)(254 - se) << 23)
-                     : (se == 254 ? __uint_as_float(0x00400000u) : 0.0f);
-  };
-  const float inv0 = recip(ebase);
-  const float inv1 = recip(ebase + 1);
+  // exact reciprocals of the pair scales 2^(se-127), se = ebase + micro
+  const float inv0 = pair_recip(ebase);
+  const float inv1 = pair_recip(ebase + 1);
   int qi[16];
-  uint32_t mb[8];
+  bool mb[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const bool mi = pa[k] > thr;
@@ -323,7 +336,7 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16
       // sign of v (v < 0 -> negative level; -0.0 gives level 0 either way)
       qi[2 * k + i] = (int)copysignf(lvl, v[2 * k + i]);
     }
-    mb[k] = mi ? 1u : 0u;
+    mb[k] = mi;
   }
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
@@ -335,52 +348,91 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16
   eb_out = (uint32_t)eb;
 }
 
-// Encode 16 values in the counter mode: T = v * 2^(143 - se) with se = ebase + micro (one exact
-// fp32 scaling, = v / pair_scale * 2^16), clamped to +-M*2^16, truncated toward zero; the level
-// (T + u16) >> 16 is byte 2 of the 32-bit sum, which the packing picks directly.
-template <int FB, int LY>
-__device__ __forceinline__ void encode16_dither(const float (&v)[16], const uint32_t (&pw)[8],
+// Encode 16 values in the counter mode. With q = v / pair_scale (signed) and the element's 16-bit
+// draw u16, t = RN(q + 192 + u16 * 2^-16) is one fma: v times the exact reciprocal of the pair
+// scale, plus 192 + u16 * 2^-16 made from the draw's bits (0x43400000 | u16). t lies in
+// [129, 256), where the fp32 spacing is exactly 2^-16, so byte 2 of its bits is
+// floor(t) - 128 = level + 64, level = floor(RN_{2^-16}(q + u16 * 2^-16)) in [-M, M]; a carry-free
+// byte fix turns level + 64 into the int8 level. Blocks whose exponent came from the exact rule
+// (see block_exponent), where |q| may exceed M, clamp t to [192 - M, 193 + M - 2^-16]: the same
+// levels as clamping q to [-M, M] first (floor(M + u) = M, floor(-M + u) = -M).
+// word(k) returns the hash word of pair k (its low half is the even element's draw, its high
+// half the odd element's). Each word is made just before its two fmas use it, and the next word
+// waits for them: computed all at once, the eight words and the block's values were live
+// together (91 VGPRs in the reference layout's row kernel instead of 77).
+template <int FB, int LY, class WordFn>
+__device__ __forceinline__ void encode16_dither(const float (&v)[16], WordFn&& word,
                                                 uint32_t (&qw)[4], uint32_t (&mw)[2],
                                                 uint32_t& eb_out) {
 #pragma clang fp contract(off)
   constexpr float M = FB == 8 ? 63.0f : 7.0f;
-  constexpr float MT = M * 65536.0f;
   float pa[8];
   const float amax = pair_maxima(v, pa);
   int eb, ebase;
   const bool band = block_exponent_fast<FB>(amax, eb, ebase);
   const float thr = M * __uint_as_float((uint32_t)ebase << 23);
-  const int sh0 = pin(143 - ebase);
-  const int sh1 = pin(142 - ebase);
+  // pair_recip(ebase) and pair_recip(ebase + 1) without branches (ebase <= 254)
+  const float inv0 = pin(ebase <= 253 ? __uint_as_float((uint32_t)(254 - ebase) << 23)
+                                      : __uint_as_float(0x00400000u));
+  const float inv1 = pin(ebase <= 253 ? inv0 * 0.5f : 0.0f);
   float t[16];
-  uint32_t mb[8];
+  bool mb[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const bool mi = pa[k] > thr;
-    const int sh = mi ? sh1 : sh0;
-    t[2 * k] = ldexpf(v[2 * k], sh);
-    t[2 * k + 1] = ldexpf(v[2 * k + 1], sh);
-    mb[k] = mi ? 1u : 0u;
+    const float inv = mi ? inv1 : inv0;
+    const uint32_t w = word(k);
+    t[2 * k] = __builtin_fmaf(v[2 * k], inv, __uint_as_float((w & 0xffffu) | 0x43400000u));
+    t[2 * k + 1] = __builtin_fmaf(v[2 * k + 1], inv, __uint_as_float((w >> 16) | 0x43400000u));
+    word.after(t[2 * k], t[2 * k + 1]);
+    mb[k] = mi;
   }
-  if (band) {  // rare: the exponent came from the exact rule (see block_exponent)
+  if (band) {  // rare
 #pragma unroll
-    for (int i = 0; i < 16; ++i) t[i] = __builtin_amdgcn_fmed3f(t[i], -MT, MT);
-  }
-  int sum[16];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    sum[2 * k] = add_word0((int)t[2 * k], pw[k]);
-    sum[2 * k + 1] = add_word1((int)t[2 * k + 1], pw[k]);
+    for (int i = 0; i < 16; ++i) {
+      t[i] = __builtin_amdgcn_fmed3f(t[i], 192.0f - M, 193.0f + M - 0x1p-16f);
+    }
   }
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)sum[4 * w + 1], (uint32_t)sum[4 * w], 0x0c0c0602u);
-    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)sum[4 * w + 3], (uint32_t)sum[4 * w + 2], 0x06020c0cu);
-    qw[w] = lo | hi;
+    const uint32_t lo = __builtin_amdgcn_perm(__float_as_uint(t[4 * w + 1]),
+                                              __float_as_uint(t[4 * w]), 0x0c0c0602u);
+    const uint32_t hi = __builtin_amdgcn_perm(__float_as_uint(t[4 * w + 3]),
+                                              __float_as_uint(t[4 * w + 2]), 0x06020c0cu);
+    // bytes b = level + 64 in [1, 127] -> (b - 64) mod 256 = (b + 64) ^ 128, where b + 64 <= 191
+    // stays inside its byte (lo and hi hold disjoint bytes, so their sum is their union: one
+    // v_add3_u32, which the compiler would split into an or and an add)
+    uint32_t b;
+    asm("v_add3_u32 %0, %1, %2, %3" : "=v"(b) : "v"(lo), "v"(hi), "s"(sgpr_const(0x40404040u)));
+    qw[w] = b ^ 0x80808080u;
   }
   pack_block<LY>(qw, mw, mb);
   eb_out = (uint32_t)eb;
 }
+
+// Hash words of a block for encode16_dither: from a precomputed array (the general kernel), or
+// hashed on demand from the block's pair-counter base (the row kernel: base = (lo32 of the first
+// pair counter) ^ K_hi after lowbias32's first xorshift, the block's pairs differing only in the
+// low 3 bits). after() makes the next word wait for the previous pair's fmas.
+struct ArrayWords {
+  const uint32_t (&pw)[8];
+  __device__ __forceinline__ uint32_t operator()(int k) const { return pw[k]; }
+  __device__ __forceinline__ void after(float, float) const {}
+};
+
+struct HashWords {
+  uint32_t base;
+  __device__ __forceinline__ uint32_t operator()(int k) const {
+    uint32_t x = base ^ (uint32_t)k;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    return x ^ (x >> 16);
+  }
+  __device__ __forceinline__ void after(float a, float b) {
+    asm volatile("" : "+v"(base) : "v"(a), "v"(b));
+  }
+};
 
 // Raw words of one block at q / mi / e (VEC: q and mi aligned to their block size).
 template <bool VEC, int LY>
@@ -486,7 +538,7 @@ __device__ __forceinline__ void encode_block(const float (&v)[16], const View& u
   if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
     uint32_t pw[8];
     block_words(key, c0, pw);
-    encode16_dither<FB, LY>(v, pw, qw, mw, eb);
+    encode16_dither<FB, LY>(v, ArrayWords{pw}, qw, mw, eb);
   } else {
     float u16[16];
     block_u16<RMODE>(uni, b, h, pp, n0, u16);
@@ -732,13 +784,14 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
     for (int i = 0; i < 16; ++i) ypart = fmaf(hv[i], Cv[i], ypart);
     float y = row_sum<BPR_LOG2>(ypart);
     if (p.has_D) y += xv * hs.D;
-    if (p.has_z) y *= zs[r];
+    y *= zs[r];  // 1.0 without z
     if (act && blk == 0) {
       const uint32_t oo = (uint32_t)pp * p.out_row_bytes;
       if (p.out.dtype == LQ_F32) {
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), hb.out, oo, 0, 0);
-      } else if (p.out.dtype == LQ_BF16) {
-        __builtin_amdgcn_raw_buffer_store_b16(float_to_bf16_bits(y), hb.out, oo, 0, 0);
+      } else if (p.out.dtype == LQ_BF16) {  // the hardware's round-to-nearest-even convert
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (__bf16)y), hb.out, oo,
+                                              0, 0);
       } else {
         __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)y), hb.out,
                                               oo, 0, 0);
@@ -751,16 +804,7 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
       const uint32_t idx = ((uint32_t)((b * p.H + h) * P + pp) * N + n0) >> 1;
       uint32_t base = (p.lo_base + idx) ^ p.kh;
       base ^= base >> 16;
-      uint32_t pw[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        uint32_t x = base ^ (uint32_t)k;
-        x *= 0x7feb352du;
-        x ^= x >> 15;
-        x *= 0x846ca68bu;
-        pw[k] = x ^ (x >> 16);
-      }
-      encode16_dither<FB, LY>(hv, pw, qo, mo, eo);
+      encode16_dither<FB, LY>(hv, HashWords{base}, qo, mo, eo);
     } else {
       float u16[16];
       if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {

@@ -15,11 +15,16 @@ Rounding modes: nearest-even (torch.round, initial encode ms.py:568), half-up fl
 (deterministic writeback ms.py:201, 482, 531), stochastic floor(qa) + (u < qa - floor(qa))
 (ms.py:196-199, 528-530) with u from a supplied tensor (ROUND_SR_UNIFORM, the reference's
 formula), and the counter mode ROUND_SR_COUNTER, which replaces the reference's Triton tl.rand
-draw by oracle.rng's 16-bit draws u16 used as a fixed-point dither:
-    T     = trunc(clamp(v * 2^16 / (base * 2^micro), -M*2^16, M*2^16))   (signed, one fp32 scaling)
-    level = floor((T + u16) / 2^16)
-which rounds |v| up with probability floor(frac(qa) * 2^16) / 2^16 (frac truncated to 16 bits,
-bias below 2^-16 of one step) on both signs, and never leaves [-M, M].
+draw by oracle.rng's 16-bit draws u16 used as a dither on a 2^-16 grid:
+    qs    = v / (base * 2^micro)                                  (signed, exact)
+    t     = fp32(192 + u16 * 2^-16 + qs)                          (one rounding: the kernel's fma)
+    level = floor(clamp(t, 192 - M, 193 + M - 2^-16)) - 192
+t lies in [128, 256), where the fp32 spacing is 2^-16, so t is qs + u16 * 2^-16 rounded to that
+grid (ties to even) plus 192. For v >= 0 it rounds |v| up for floor(F + 1/2) of the 2^16 draws,
+for v < 0 for ceil(F - 1/2), F = frac(|qs|) * 2^16: F rounded to the nearest integer, so the
+bias stays within half a grid step (2^-17 of a level step), on both signs; the clamp (a no-op
+unless |qs| > M, which only a block inside the exponent's rounding band can give) keeps the
+level in [-M, M].
 
 ceil(log2(t)) is defined as the ceiling of the correctly rounded fp32 log2 of t. For a t with
 unbiased exponent E and mantissa field j, that ceiling is E when j == 0, E when the fp32 value
@@ -32,8 +37,9 @@ reachable E; ceil_log2 against exact integer comparisons away from the rounding 
 invariants (|q| <= M, e in [1, 254], micro in {0,1}); half-step error bound of the nearest-even
 decode; the all-zero block (e = 28, q = 0); exact powers of two; the floor(q + 0.5) double
 rounding case; stochastic rounding with u = 0 (ceil) and u -> 1 (floor) and its unbiasedness;
-the counter dither by enumerating all 2^16 draws (round-up count = floor(frac * 2^16) exactly,
-for both signs, exact fractions) and its clamp;
+the counter dither by enumerating all 2^16 draws (the round-up count against exact rational
+arithmetic on the 2^-16 grid, for both signs, ties included) and its clamp, and random values
+against a Fraction restatement;
 the update's closed forms (dt = 0 leaves h unchanged so the writeback is a pure re-encode;
 A = 0 gives h + dt*B*x; softplus threshold at 20) against an independent float64 evaluation.
 bf16_state_update (drift baseline) restates mamba_ssm's selective_state_update, a dependency
@@ -126,16 +132,20 @@ def mx_encode(state, format_bits: int, round_mode: int = ROUND_NEAREST_EVEN,
     pair_scale = (base[..., None] * np.where(micro, np.float32(2.0), np.float32(1.0))).astype(
         np.float32)
     if round_mode == ROUND_SR_COUNTER:
-        # fixed-point dither: T = v / pair_scale * 2^16 as one fp32 scaling (the pair scale is a
-        # power of two, 2^(se-127) with se = exponent + micro and exponent 127 for a zero block),
-        # clamped to +-M*2^16 and truncated toward zero; level = floor((T + u16) / 2^16).
+        # dither on the 2^-16 grid: qs = v / pair_scale exactly (the pair scale is a power of two,
+        # 2^(se-127) with se = exponent + micro and exponent 127 for a zero block);
+        # t = fp32(192 + u16 * 2^-16 + qs), level = floor(t) - 192 after the clamp. The float64
+        # sum is exact for |qs| >= 2^-22 (at most 53 bits from 2^7 down to qs's last bit); below
+        # that qs is under a quarter of the fp32 spacing of t, so either way t = 192 + u16 * 2^-16.
         se = np.where(amax == 0, 127, biased)[..., None] + micro.astype(np.int64)
-        t16 = np.ldexp(pairs, (143 - se)[..., None].astype(np.int32)).astype(np.float32)
-        t16 = np.clip(t16, -m * np.float32(65536.0), m * np.float32(65536.0))
+        qs = np.ldexp(pairs.astype(np.float64), (127 - se)[..., None].astype(np.int32))
         if u16 is None:
             u16 = rng.state_u16(seed, rng_offset, v.shape)
-        u16 = np.asarray(u16).reshape(pairs.shape).astype(np.int64)
-        level = (np.trunc(t16).astype(np.int64) + u16) >> 16
+        u16 = np.asarray(u16).reshape(pairs.shape).astype(np.float64)
+        with np.errstate(invalid="ignore"):
+            t = (192.0 + u16 * 2.0**-16 + qs).astype(np.float32)
+        t = np.clip(t, np.float32(192.0) - m, np.float32(193.0 - 2.0**-16) + m)
+        level = np.floor(t).astype(np.int64) - 192
         q = level.reshape(v.shape).astype(np.int8)
         shared = biased.astype(np.uint8)
         micro_u8 = micro.astype(np.uint8).reshape(*v.shape[:-1], n // PAIR)

@@ -13,7 +13,8 @@ their own counter-based generator, restated here bit for bit:
 
 lowbias32 is the 32-bit integer mixer x ^= x>>16; x *= 0x7feb352d; x ^= x>>15; x *= 0x846ca68b;
 x ^= x>>16 (C. Wellons, "hash prospector", public domain). The even element of a pair takes the
-low half. oracle.mx_state uses u16 as a fixed-point dither (bias below 2^-16 of one step).
+low half. oracle.mx_state adds u16 * 2^-16 to the scaled value on a 2^-16 grid and floors
+(bias within 2^-17 of one level step).
 
 Pinning (tests/test_oracle_mx.py): the vectorized numpy version against a scalar pure-Python
 version, known-answer vectors in tests/golden/rng_vectors.json, lowbias32 bijectivity on a

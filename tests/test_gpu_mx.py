@@ -324,3 +324,47 @@ def test_full_size_b64_uniform_update_sampled_groups(gpu, fb):
                                      dt_softplus=True)
         assert_mx_writeback([a[bs, hs].cpu().numpy() for a in st], (rq, re_, rm), rh, mag, fb,
                             2, uniform=uni[bs, hs].cpu(), what=f"state b{b} g{g}")
+
+
+@pytest.mark.parametrize("fb", [8, 4])
+@pytest.mark.parametrize("mode", [_abi.ROUND_SR_UNIFORM, _abi.ROUND_SR_COUNTER])
+def test_config3_batch1_full_layer_every_group(gpu, diag, fb, mode):
+    """BASELINE configs 3 (MX8) and 4 (MX4) at batch 1 on the full Nemotron-H layer (128 heads x
+    64 x 128, 8 groups): h0 ~ N(0, 0.5) encoded by the initial encoder, x ~ N(0, 1),
+    dt = softplus(N(0, 1)) per head (passed with dt_softplus off), A = -exp(U(0, 2)), B, C ~ N(0, 1)
+    per group, D ~ N(0, 1); the seeded supplied-uniform writeback (the configurations' own
+    rounding) or the counter generator; the model's layout, so the row kernel (required). The
+    whole state -- every group -- against the oracle: y within 2e-3, the writeback to the
+    assert_mx_writeback bar."""
+    diag.set("LQ_MX_REQUIRE_ROWS")
+    bsz, nh, p_, n, ng = 1, 128, 64, 128, 8
+    shape = (bsz, nh, p_, n)
+    g = torch.Generator().manual_seed(300 + fb + mode)
+    h0 = torch.randn(shape, generator=g) * 0.5
+    t = dict(
+        x=torch.randn(bsz, nh, p_, generator=g).to(torch.bfloat16),
+        dt=torch.nn.functional.softplus(torch.randn(bsz, nh, 1, generator=g)).expand(bsz, nh, p_),
+        A=(-torch.exp(torch.rand(nh, generator=g) * 2))[:, None, None].expand(nh, p_, n),
+        B=torch.randn(bsz, ng, n, generator=g).to(torch.bfloat16),
+        C=torch.randn(bsz, ng, n, generator=g).to(torch.bfloat16),
+        D=torch.randn(nh, generator=g)[:, None].expand(nh, p_),
+    )
+    uni = torch.rand(shape, generator=g) if mode == _abi.ROUND_SR_UNIFORM else None
+    dev = {k: to_device(v, gpu) for k, v in t.items()}
+    st = _mx_tensors(shape, gpu)
+    _abi.mx_encode(h0.to(gpu), *st, fb, _abi.ROUND_NEAREST_EVEN)
+    q0, e0, m0 = (a.cpu().numpy() for a in st)
+    assert all(np.array_equal(a, b) for a, b in zip((q0, e0, m0), omx.mx_encode(h0.numpy(), fb)))
+    out = torch.empty(bsz, nh, p_, device=gpu)
+    seed, off = 1234, 7 * int(np.prod(shape))
+    _abi.mx_state_update(*st, dev["x"], dev["dt"], None, dev["A"], dev["B"], dev["C"], dev["D"],
+                         None, out, fb, False, mode, None if uni is None else uni.to(gpu),
+                         seed=seed, rng_offset=off)
+    torch.cuda.synchronize()
+    args = (t["x"], t["dt"], t["A"], t["B"], t["C"])
+    rq, re_, rm, ry, rh = omx.mx_update(q0, e0, m0, *args, D=t["D"], format_bits=fb,
+                                        round_mode=mode, uniform=uni, seed=seed, rng_offset=off)
+    assert_close_rel(out.cpu(), ry, what=f"y mx{fb} mode {mode}")
+    mag = update_term_magnitudes(omx.mx_decode(q0, e0, m0), *args)
+    assert_mx_writeback([a.cpu().numpy() for a in st], (rq, re_, rm), rh, mag, fb, mode,
+                        uniform=uni, seed=seed, rng_offset=off, what=f"state mx{fb} mode {mode}")

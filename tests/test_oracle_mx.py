@@ -3,6 +3,7 @@ ceil(log2) rule against 60-digit arithmetic, encoder invariants and special case
 closed forms against an independent float64 evaluation, and the counter generator against a
 scalar implementation and committed known-answer vectors."""
 import json
+import math
 from fractions import Fraction
 from pathlib import Path
 
@@ -113,11 +114,32 @@ def test_stochastic_rounding_extremes_and_unbiasedness():
     assert bias.mean() < 0.03 and bias.max() < 0.2
 
 
-def test_counter_dither_enumerates_to_the_truncated_fraction():
-    """All 2^16 draws for one value: the round-up count is floor(frac(qa) * 2^16), exactly, on
-    both signs; the pair (7, x) of a block with absmax 7 has scale 1, so qa = |x|."""
+def _grid_round(x: Fraction) -> Fraction:
+    """x rounded to the nearest multiple of 2^-16, ties to the even multiple."""
+    y = x * 65536
+    lo = y.numerator // y.denominator
+    r = y - lo
+    k = lo + (1 if r > Fraction(1, 2) or (r == Fraction(1, 2) and lo % 2 == 1) else 0)
+    return Fraction(k, 65536)
+
+
+def _counter_level(qs: Fraction, u16: int, m: int) -> int:
+    """The counter mode's level in exact rational arithmetic: qs + u16 * 2^-16 on the 2^-16
+    grid, clamped to [-M, M + 1 - 2^-16], floored."""
+    t = _grid_round(qs + Fraction(u16, 65536))
+    t = min(max(t, Fraction(-m)), Fraction(m + 1) - Fraction(1, 65536))
+    return t.numerator // t.denominator
+
+
+def test_counter_dither_enumerates_to_the_rounded_fraction():
+    """All 2^16 draws for one value: with F = frac(qa) * 2^16, |v| rounds up for floor(F + 1/2)
+    draws when v > 0 and ceil(F - 1/2) when v < 0 (F to the nearest integer, a tie going to the
+    even grid point), checked against exact rational arithmetic; the pair (7, x) of a block with
+    absmax 7 has scale 1, so qa = |x|."""
     u = np.arange(1 << 16, dtype=np.uint32)
-    for x in (2.3, 0.7, 6.99999, 1.0 + 2.0**-20, 5.0, 0.0, 3.0 + 2.0**-16 + 2.0**-17):
+    xs = (2.3, 0.7, 6.99999, 1.0 + 2.0**-20, 5.0, 0.0, 3.0 + 2.0**-16 + 2.0**-17,
+          4.0 + 2.0**-17, 2.0 - 2.0**-18, 1.0 + 3 * 2.0**-17)
+    for x in xs:
         for sign in (1.0, -1.0):
             xv = np.float32(sign * x)
             v = np.zeros((u.size, 16), np.float32)
@@ -129,18 +151,42 @@ def test_counter_dither_enumerates_to_the_truncated_fraction():
             assert (e == 126).all() and (m[:, 0] == 1).all()
             mag = Fraction(float(abs(xv)))
             fl = int(mag)
-            want_up = int((mag - fl) * 65536)
+            f16 = (mag - fl) * 65536
+            half = Fraction(1, 2)
+            if sign > 0:
+                want_up = int(math.floor(f16 + half))
+            else:
+                want_up = int(math.ceil(f16 - half))
             lv = np.abs(q[:, 1].astype(np.int64))
             assert set(np.unique(lv)) <= {fl, fl + 1}
             assert int((lv == fl + 1).sum()) == want_up, (x, sign)
             if xv != 0:
                 assert (np.sign(q[:, 1][lv > 0]) == np.sign(xv)).all()
+            # level by level against the rational restatement (every 97th draw)
+            for k in range(0, 1 << 16, 97):
+                assert q[k, 1] == _counter_level(Fraction(float(xv)), k, 7), (x, sign, k)
+
+
+def test_counter_dither_random_values_against_rationals():
+    """Random blocks (both formats, many binades, micro pairs) level by level against the
+    rational restatement, with the oracle's exponents and micro flags."""
+    rs = np.random.default_rng(5)
+    for fb, mant in ((4, 7), (8, 63)):
+        v = (rs.standard_normal((64, 16)) * np.exp2(rs.integers(-30, 30, (64, 1)))).astype(np.float32)
+        v[::7, 3] *= 3.0  # wide pairs: micro flags set
+        draws = rs.integers(0, 1 << 16, v.shape).astype(np.uint32)
+        q, e, m = mx.mx_encode(v, fb, mx.ROUND_SR_COUNTER, u16=draws)
+        for i in range(v.shape[0]):
+            for j in range(16):
+                se = int(e[i, 0]) + int(m[i, j // 2])
+                qs = Fraction(float(v[i, j])) / Fraction(2) ** (se - 127)
+                assert q[i, j] == _counter_level(qs, int(draws[i, j]), mant), (fb, i, j)
 
 
 def test_counter_dither_clamps_at_the_mantissa_limit():
     """A block whose rounded absmax/14 sits 20 ulps above 2^-80 keeps e = -80 (inside the
     correctly rounded log2 band), so the micro pair's qa = 7 + 140*2^-23 exceeds M = 7 by more
-    than 2^-16: without the clamp the largest draws would give level 8."""
+    than half the 2^-16 grid: without the clamp the largest draws would give level 8."""
     amax = np.float32(2.0**-77 * (1.75 + 35 * 2.0**-23))
     assert float(amax) / 14 == 2.0**-80 * (1 + 20 * 2.0**-23)
     u = np.arange(1 << 16, dtype=np.uint32)
@@ -152,8 +198,9 @@ def test_counter_dither_clamps_at_the_mantissa_limit():
         q, e, m = mx.mx_encode(v, 4, mx.ROUND_SR_COUNTER, u16=draws)
         assert (e == 127 - 80).all() and (m[:, 0] == 1).all()
         assert (q[:, 0] == int(sign * 7)).all()
-    t16 = Fraction(float(amax)) * 2**79 * 65536
-    assert (int(t16) + 65535) >> 16 == 8
+    qa = Fraction(float(amax)) * 2**79
+    t = _grid_round(qa + Fraction(65535, 65536))
+    assert t.numerator // t.denominator == 8
 
 
 def _independent_update(h, x, dt, A, B, C, D, z, dt_bias, softplus):
