@@ -717,14 +717,14 @@ __device__ __forceinline__ void load_rows(const MxUpdateParams& p, const HeadBuf
 }
 
 // Update, y, and writeback encode of the R rows held in L. bdp and cvp point to the lane's 16
-// values of B * dt and C in LDS. With BC_REREAD they are read again for every row instead of
-// once into 32 VGPRs: the compact layouts' 4-row form then fits 74 VGPRs (6 waves per SIMD
-// instead of 5; MX4 at batch 64 38.7 -> 37.1 us, batch 128 72.0 -> 68.1 us on one box), while
-// the reference layout's 2-row form keeps the register copy (7 waves per SIMD without it ran
-// 42.5 against 39.6 us).
+// values of B * dt and C in LDS, read again for every row instead of once into 32 VGPRs: the
+// compact layouts' 4-row form then fits 74 VGPRs (6 waves per SIMD instead of 5; MX4 at batch 64
+// 38.7 -> 37.1 us, batch 128 72.0 -> 68.1 us on one box), the reference layout's 2-row form 67
+// (7 waves instead of 6; MX4 at batch 64 39.0-39.2 -> 38.3-38.6 us on one box, three alternated
+// runs; with the earlier, VALU-heavier encoder it had been slower, 42.5 against 39.6 us).
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-template <int FB, int RMODE, int BPR_LOG2, int R, int SLOTS, int LY, bool BC_REREAD>
+template <int FB, int RMODE, int BPR_LOG2, int R, int SLOTS, int LY>
 __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadBufs& hb, int b,
                                             int h, int row0, int slot, int blk,
                                             const RowLoads<R>& L, const float* bdp,
@@ -745,7 +745,6 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
       }
     }
   };
-  if constexpr (!BC_REREAD) read_bc();
   // x and z of every row converted before the first store: converted inside the row loop, a
   // later row's conversion (a dtype branch) came after the earlier rows' stores, and the wait the
   // compiler placed for its load there (vmcnt counts stores too) also waited for those stores
@@ -758,10 +757,8 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    if constexpr (BC_REREAD) {
-      asm volatile("" ::: "memory");  // keeps the compiler from reusing the previous row's copy
-      read_bc();
-    }
+    asm volatile("" ::: "memory");  // keeps the compiler from reusing the previous row's copy
+    read_bc();
     const int pp = row0 + r * SLOTS + slot;
     const bool act = pp < P;
     const uint32_t pc = (uint32_t)min(pp, P - 1);
@@ -894,8 +891,8 @@ void mx_update_rows_kernel(MxUpdateParams p) {
   hs.dt = 0.0f;  // folded into B * dt
   hs.dA = s_hs[0];
   hs.D = s_hs[1];
-  update_rows<FB, RMODE, BPR_LOG2, R, SLOTS, LY, (LY != LAYOUT_REF)>(p, hb, b, h, row0, slot, blk, L,
-                                                              &s_bd[n0], &s_c[n0], hs);
+  update_rows<FB, RMODE, BPR_LOG2, R, SLOTS, LY>(p, hb, b, h, row0, slot, blk, L, &s_bd[n0],
+                                                 &s_c[n0], hs);
 }
 
 template <int FB, int RMODE, bool VEC, int LY>
@@ -1165,9 +1162,9 @@ static void dispatch_encode(const MxCodecParams& p, int rmode, bool vec, dim3 gr
 
 // Rows kernel geometry: R rows per lane, THREADS threads, one (batch, head) slice of up to
 // R * THREADS / (N/16) rows per workgroup (64 rows = one Nemotron-H head at N = 128). The reference
-// layout keeps 2 rows per lane (78 VGPRs, 6 waves per SIMD: its 212 MB per call at batch 64 need
-// the waves to hide memory latency; 4 rows per lane take 100 VGPRs, 4 waves, and ran 42.2 against
-// 41.4 us). The compact layouts move 2.5x fewer bytes and are bound by their arithmetic, so 4 rows
+// layout keeps 2 rows per lane (67 VGPRs, 7 waves per SIMD: its 212 MB per call at batch 64 need
+// the waves to hide memory latency; 4 rows per lane take 87 VGPRs, 5 waves, and with an earlier
+// build ran 42.2 against 41.4 us). The compact layouts move 2.5x fewer bytes and are bound by their arithmetic, so 4 rows
 // per lane share the per-lane setup (head scalars, B and C) over twice the rows: 41.1 -> 38.9 us
 // for MX4 at batch 64 (91 VGPRs, 5 waves per SIMD). The supplied-uniform mode keeps 2 rows per
 // lane everywhere: its 16 uniforms per row would take 155-161 VGPRs at 4 rows.
