@@ -105,7 +105,8 @@ enum {
   LQ_DIAG_MX_REQUIRE_ROWS = 1u << 5,
   LQ_DIAG_SSM_FORCE_GENERIC = 1u << 6,
   LQ_DIAG_SSM_REQUIRE_ROWS = 1u << 7,
-  LQ_DIAG_ALL = (1u << 8) - 1
+  LQ_DIAG_ATTN_MERGE_KERNEL = 1u << 8, /* split-K partials merged by a second launch, not folded */
+  LQ_DIAG_ALL = (1u << 9) - 1
 };
 
 /* The current LQ_DIAG_* bits. */
@@ -142,8 +143,13 @@ int lq_int4_pack_kv_pair(const lq_tensor* k, const lq_tensor* v, const lq_tensor
 /*
  * Workspace bytes that lq_int4_decode_attention needs for this shape (0 if none).
  * No counterpart in the reference (its decode kernel has no split-K); it sizes the split-K
- * partials of the kernel below.
+ * partials of the kernel below. A workspace (256-byte aligned) starts with
+ * LQ_DECODE_ATTENTION_COUNTER_BYTES of arrival counters, which must be zero before the workspace
+ * is first used (e.g. allocate it zeroed); every call leaves them zero again, so a workspace can be
+ * reused across calls of any shape, in order on one stream, and under HIP graph replay. (A call
+ * that does not run to completion, e.g. one whose kernel is aborted, can leave them non-zero.)
  */
+#define LQ_DECODE_ATTENTION_COUNTER_BYTES (64u << 10)
 size_t lq_int4_decode_attention_workspace(int64_t batch, int64_t n_q_heads, int64_t n_kv_heads,
                                           int64_t head_dim, int64_t seq_len, int group_size);
 
@@ -195,8 +201,9 @@ int lq_int4_decode_attention_pack(const lq_tensor* q, const lq_tensor* k_new,
  * shape needs). Calls no allocating routine.
  * No counterpart in the reference: for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * Every call on one GPU shares that GPU's buffer and it keeps the last call's partials (nothing
- * in it has to start at zero): calls that overlap on one GPU -- on different streams, or from
+ * Every call on one GPU shares that GPU's buffer; it keeps the last call's partials, and its
+ * arrival counters (zero when the library loads) are left zero by every call: calls that overlap
+ * on one GPU -- on different streams, or from
  * different host threads -- race and must be serialized by the caller; calls in order on one
  * stream are safe. The buffer is on the device that runs `stream`. The first call on a device
  * resolves the buffer's device address (hipGetSymbolAddress); make that call outside any HIP

@@ -38,6 +38,7 @@ DIAG_BITS = {
     "LQ_MX_REQUIRE_ROWS": 1 << 5,
     "LQ_SSM_FORCE_GENERIC": 1 << 6,
     "LQ_SSM_REQUIRE_ROWS": 1 << 7,
+    "LQ_ATTN_MERGE_KERNEL": 1 << 8,
 }
 
 DTYPE_CODES = {
@@ -259,7 +260,9 @@ def int4_pack_kv_pair(k: torch.Tensor, v: torch.Tensor, k_packed: torch.Tensor,
 
 
 class _Workspace:
-    """Per (device, stream) scratch buffer for the split-K partials, grown on demand."""
+    """Per (device, stream) scratch buffer for the split-K partials, grown on demand. Allocated
+    zeroed: the library's arrival counters at its start must be zero before first use (every
+    call leaves them zero)."""
 
     def __init__(self):
         self._bufs: dict[tuple[int, int], torch.Tensor] = {}
@@ -272,7 +275,7 @@ class _Workspace:
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
-                buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 

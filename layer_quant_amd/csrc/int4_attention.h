@@ -21,6 +21,8 @@ struct AttnParams {
   float* ws_m;
   float* ws_l;
   float* ws_acc;
+  uint32_t* ws_cnt;  // arrival counters of the (batch, KV head) units (fold)
+  int fold;          // the fast kernel merges its own splits (no attn_merge_kernel launch)
   int B, Hq, Hkv, D, g, nrep;
   int64_t S;
   int nsplit;     // workgroup splits along the keys
@@ -37,7 +39,15 @@ struct SplitPlan {
   int64_t chunk;
 };
 
+// Split-K workspace layout: arrival counters in a fixed area at the start (so that every shape
+// finds them at the same place; zero before a workspace's first use, left zero by every call),
+// then the partials m [slots], l [slots], acc [slots][D], each array 256-byte aligned.
+constexpr int ARRIVAL_UNITS = 16384;  // (batch, KV head) units a folded merge can count
+constexpr size_t ARRIVAL_BYTES = (size_t)ARRIVAL_UNITS * 4;
+static_assert(ARRIVAL_BYTES == LQ_DECODE_ATTENTION_COUNTER_BYTES, "header and kernels agree");
+
 // fast path (int4_attention_mfma.hip)
+bool fast_fold_fits(int nrep, int nsplit);
 bool fast_path_shape_ok(int64_t head_dim, int group_size, int64_t n_q_heads, int64_t n_kv_heads);
 bool fast_path_ok(const AttnParams& p);
 SplitPlan plan_fast(int64_t B, int64_t Hkv, int64_t S);

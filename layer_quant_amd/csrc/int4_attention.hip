@@ -8,7 +8,9 @@
 //     (batch, query head, split), fp32 VALU throughout.
 // Scores follow the reference: s_n = (q . k_n) * log2(e)/sqrt(D) (+ mask_n), exp2-domain online
 // softmax; keys at or beyond the mask length get -inf. Splits write (m, l, acc[D]) partials into
-// the caller's workspace and attn_merge_kernel combines them; a single split writes out directly.
+// the caller's workspace; the MFMA kernel's last workgroup of each (batch, KV head) merges them
+// (counted by arrival counters at the start of the workspace), otherwise attn_merge_kernel does;
+// a single split writes out directly.
 // lq_int4_decode_attention_pack first packs the new token into cache row seq_len - 1 (the
 // reference's _pack_kv_into_cache at :477-515): inside attn_fast_kernel on the MFMA path, by the
 // pack kernel before the generic one otherwise.
@@ -228,18 +230,19 @@ static SplitPlan plan_generic(int64_t B, int64_t Hq, int64_t S) {
 static size_t partial_bytes(int64_t B, int64_t Hq, int64_t D, int nsplit) {
   if (nsplit <= 1) return 0;
   const size_t slots = (size_t)(B * Hq) * (size_t)nsplit;
-  // m and l arrays, then acc; each array rounded up to 256 bytes
+  // the arrival counters, then the m and l arrays, then acc; each rounded up to 256 bytes
   const size_t ml = ((slots * 4 + 255) / 256) * 256;
-  return 2 * ml + slots * (size_t)D * 4;
+  return ARRIVAL_BYTES + 2 * ml + slots * (size_t)D * 4;
 }
 
 static void carve_workspace(AttnParams& p, void* ws) {
   const size_t slots = (size_t)(p.B * p.Hq) * (size_t)p.nsplit;
   const size_t ml = ((slots * 4 + 255) / 256) * 256;
   char* base = (char*)ws;
-  p.ws_m = (float*)base;
-  p.ws_l = (float*)(base + ml);
-  p.ws_acc = (float*)(base + 2 * ml);
+  p.ws_cnt = (uint32_t*)base;
+  p.ws_m = (float*)(base + ARRIVAL_BYTES);
+  p.ws_l = (float*)(base + ARRIVAL_BYTES + ml);
+  p.ws_acc = (float*)(base + ARRIVAL_BYTES + 2 * ml);
 }
 
 // Split-K partials of lq_int4_decode_attention_noalloc: a static buffer on every device the
@@ -520,6 +523,9 @@ static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
       return rc;
     }
   }
+  // the MFMA kernel merges its own splits when the unit count fits the arrival counters
+  p.fold = fast && p.nsplit > 1 && B * Hkv <= ARRIVAL_UNITS &&
+           fast_fold_fits(num_key_value_groups, p.nsplit) && !diag(LQ_DIAG_ATTN_MERGE_KERNEL);
   if (fast) {
     if ((rc = launch_fast(p, st)) != LQ_OK) return rc;
   } else {
@@ -527,7 +533,7 @@ static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
                        dim3(64), 0, st, p);
     if ((rc = check_launch("lq_int4_decode_attention")) != LQ_OK) return rc;
   }
-  if (p.nsplit > 1) {
+  if (p.nsplit > 1 && !p.fold) {
     hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * Hq)), dim3(MERGE_THREADS), 0, st, p);
     if ((rc = check_launch("lq_int4_decode_attention merge")) != LQ_OK) return rc;
   }

@@ -240,6 +240,72 @@ __device__ __forceinline__ void issue_tile(const Rsrc& R, int tb, int S, TileLds
   }
 }
 
+// Device-coherent (agent-scope, relaxed) store and load of a split-K partial: written through to
+// where every XCD's L2 sees it, read past a possibly stale copy in this XCD's L2.
+__device__ __forceinline__ void coherent_store(float* a, float v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coherent_load(const float* a) {
+  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The folded merge handles units with NREP * nsplit <= FOLD_MAX_PARTIALS: one thread's outputs
+// then need at most FOLD_MAX_PARTIALS / 2 partial loads, all issued at once.
+constexpr int FOLD_MAX_PARTIALS = 128;
+
+// The merge of one (batch, KV head) unit's nsplit partials, by the unit's workgroup that arrived
+// last: every load goes out at once (thread t's acc partials of outputs t + 256 j over all
+// splits, and one (m, l) pair per thread for the first NREP * nsplit threads, through LDS), so
+// the merge costs one round trip of device-coherent loads. The same formulas as
+// attn_merge_kernel: M = max_s m_s, w_s = 2^(m_s - M), out = sum_s w_s acc_s / sum_s w_s l_s.
+template <int NREP>
+__device__ __forceinline__ void merge_unit(const AttnParams& p, int b, int kvh, float* s_m,
+                                           float* s_l) {
+  constexpr int OPT = (NREP * FAST_D + THREADS - 1) / THREADS;  // outputs per thread
+  constexpr int SMAX = FOLD_MAX_PARTIALS / NREP;                // splits at most
+  const int tid = threadIdx.x;
+  const int ns = p.nsplit;
+  const int64_t head0 = (int64_t)b * p.Hq + kvh * NREP;
+  float part[OPT][SMAX];
+#pragma unroll
+  for (int j = 0; j < OPT; ++j) {
+    const int o = tid + THREADS * j;
+    const int h = min(o / FAST_D, NREP - 1);
+    const int d = o % FAST_D;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      part[j][s] = (s < ns) ? coherent_load(&p.ws_acc[((head0 + h) * ns + s) * FAST_D + d]) : 0.0f;
+    }
+  }
+  if (tid < NREP * ns) {
+    s_m[tid] = coherent_load(&p.ws_m[head0 * ns + tid]);  // [h][s], h-major as in the workspace
+    s_l[tid] = coherent_load(&p.ws_l[head0 * ns + tid]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < OPT; ++j) {
+    const int o = tid + THREADS * j;
+    if (o >= NREP * FAST_D) break;
+    const int h = o / FAST_D;
+    const int d = o % FAST_D;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, s_m[h * ns + s]);
+    float L = 0.0f, a = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      if (s < ns) {
+        const float ms = s_m[h * ns + s];
+        const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
+        L += w * s_l[h * ns + s];
+        a += w * part[j][s];
+      }
+    }
+    const int qh = kvh * NREP + h;
+    store_float(p.out.data, p.out.dtype, b * p.out.s[0] + qh * p.out.s[1] + d * p.out.s[2],
+                a / L);
+  }
+}
+
 template <int NREP, int G, bool MASK>
 __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
   constexpr int LPT = tile_loads<MASK>();
@@ -593,13 +659,39 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
                   a / L);
     } else {
       const int64_t slot = ((int64_t)b * p.Hq + qh) * p.nsplit + split;
-      p.ws_acc[slot * FAST_D + d] = a;
+      coherent_store(&p.ws_acc[slot * FAST_D + d], a);
       if (d == 0) {
-        p.ws_m[slot] = M;
-        p.ws_l[slot] = L;
+        coherent_store(&p.ws_m[slot], M);
+        coherent_store(&p.ws_l[slot], L);
       }
     }
   }
+  if (p.nsplit > 1 && p.fold) {
+    // Folded split-K merge: the last of the unit's nsplit workgroups to arrive merges all of
+    // them and puts the unit's counter back to 0, so a call leaves every counter as it found it.
+    // No workgroup waits for another. The partials go through device-coherent accesses (written
+    // through past this XCD's L2, read past the merging XCD's), and each thread's stores have
+    // completed (vmcnt counts stores on gfx9) before the workgroup's arrival is counted, so the
+    // last arrival sees every split's partials. A device-scope fence instead (__threadfence:
+    // a write-back and an invalidate of the whole L2 per workgroup) made batch 1, ctx 4096 take
+    // 32.4 instead of 14.0 us.
+    __shared__ int s_last;
+    __shared__ float s_m[FOLD_MAX_PARTIALS], s_l[FOLD_MAX_PARTIALS];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      s_last = __hip_atomic_fetch_add(&p.ws_cnt[unit], 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(p.nsplit - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    merge_unit<NREP>(p, b, kvh, s_m, s_l);
+    if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+bool fast_fold_fits(int nrep, int nsplit) {
+  return (int64_t)nrep * nsplit <= FOLD_MAX_PARTIALS;
 }
 
 bool fast_path_shape_ok(int64_t head_dim, int group_size, int64_t n_q_heads,

@@ -355,3 +355,51 @@ def test_module_api_pack_then_attend(gpu):
     ref = oik.decode_attention(q, ref_cache["k_packed"], ref_cache["v_packed"],
                                ref_cache["k_scale"], ref_cache["v_scale"], steps, nrep, g)
     assert_close_rel(out.float().cpu(), ref, rtol=8e-3)
+
+
+def test_folded_split_merge_matches_merge_kernel_and_leaves_counters_zero(gpu, diag):
+    """Multi-split MFMA calls merge their partials in the kernel (the last workgroup of each
+    (batch, KV head) to arrive): over shapes with 2-64 splits, masked and not, groups 32/64/128,
+    1-16 query heads per KV head, all through one reused workspace, the output equals the
+    two-launch form's (LQ_ATTN_MERGE_KERNEL: the same partials, merged by attn_merge_kernel,
+    whose sums run in another order: within 1e-5 of the output's mean magnitude) and the
+    oracle's, and after every
+    call the workspace's arrival counters are all zero again."""
+    diag.set("LQ_ATTN_REQUIRE_FAST")
+    gen = torch.Generator(device=gpu).manual_seed(77)
+    d = 128
+    counter_words = (64 << 10) // 4
+    ws = torch.zeros(4 << 20, dtype=torch.uint8, device=gpu)
+    lib = _abi.lib()
+    cases = [(1, 8, 4, 16384, 32, False), (8, 8, 4, 2072, 64, False), (2, 8, 4, 5000, 32, True),
+             (1, 1, 16, 9000, 128, False), (3, 2, 8, 3001, 64, True), (1, 8, 2, 700, 32, False)]
+    for b, hkv, nrep, s, g, masked in cases:
+        need = lib.lq_int4_decode_attention_workspace(b, hkv * nrep, hkv, d, s, g)
+        assert need > 64 << 10, (b, s, need)  # several splits
+        kp = torch.randint(0, 256, (b, hkv, s, d // 2), dtype=torch.uint8, device=gpu, generator=gen)
+        vp = torch.randint(0, 256, (b, hkv, s, d // 2), dtype=torch.uint8, device=gpu, generator=gen)
+        ks = torch.rand(b, hkv, s, d // g, device=gpu, generator=gen) + 0.01
+        vs = torch.rand(b, hkv, s, d // g, device=gpu, generator=gen) + 0.01
+        q = torch.randn(b, hkv * nrep, 1, d, device=gpu, generator=gen).to(torch.bfloat16)
+        mask = None
+        if masked:
+            mask = torch.randn(b, 1, 1, s, device=gpu, generator=gen)
+            mask[..., s // 3: s // 2] = float("-inf")
+        outs = []
+        for merge_kernel in (False, True):
+            with _abi.diagnostic("LQ_ATTN_MERGE_KERNEL", on=merge_kernel):
+                out = torch.full((b, hkv * nrep, d), float("nan"), device=gpu)
+                rc = lib.lq_int4_decode_attention(
+                    _abi.desc(q), _abi.desc(kp), _abi.desc(vp), _abi.desc(ks), _abi.desc(vs),
+                    _abi.desc(mask), _abi.desc(out), s, nrep, g, ws.data_ptr(), ws.numel(),
+                    torch.cuda.current_stream().cuda_stream)
+                _abi.check(rc, "lq_int4_decode_attention")
+                torch.cuda.synchronize()
+                assert not ws[: counter_words * 4].view(torch.int32).any(), (b, s, merge_kernel)
+                outs.append(out)
+        assert torch.isfinite(outs[0]).all()
+        scale = outs[1].abs().mean().item()
+        torch.testing.assert_close(outs[0], outs[1], rtol=1e-5, atol=1e-5 * scale)
+        ref = oik.decode_attention(q.cpu(), kp.cpu(), vp.cpu(), ks.cpu(), vs.cpu(), s, nrep, g,
+                                   mask=None if mask is None else mask.cpu())
+        assert_close_rel(outs[0], ref, what=f"folded merge b{b} s{s} g{g}")
