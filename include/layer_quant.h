@@ -285,6 +285,25 @@ int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* shared_exp,
                        const lq_tensor* uniform, uint64_t seed, uint64_t rng_offset, void* stream);
 
 /*
+ * lq_mx_state_update with the counter offset's step on the device: the same arguments and
+ * results, with LQ_ROUND_SR_COUNTER's offset rng_offset + step[0] * B*H*P*N, where step is an
+ * int64 [1] tensor on the device that the kernel reads when it runs (the reference's offsets
+ * step*B*H*P*N with the step counter on the device; other rounding modes ignore it). A caller that
+ * captures an update in a HIP graph and advances step inside the graph (e.g. a captured add of 1)
+ * draws fresh values on every replay; with the host offset the draws of the capture would repeat.
+ * No counterpart in the reference (its step counter is a host integer, baked into every Triton
+ * launch, hybrid_quant/mamba_state_8b_kernel.py:659, 716).
+ */
+int lq_mx_state_update_device_step(const lq_tensor* q_state, const lq_tensor* shared_exp,
+                                   const lq_tensor* micro_exp, const lq_tensor* x,
+                                   const lq_tensor* dt, const lq_tensor* dt_bias,
+                                   const lq_tensor* A, const lq_tensor* B, const lq_tensor* C,
+                                   const lq_tensor* D, const lq_tensor* z, const lq_tensor* out,
+                                   int format_bits, int dt_softplus, int round_mode,
+                                   const lq_tensor* uniform, uint64_t seed, uint64_t rng_offset,
+                                   const lq_tensor* step, void* stream);
+
+/*
  * Selective-state update of an unquantized (bf16, fp16 or fp32) Mamba2 state, in place:
  *   dt = dt (+ dt_bias); dt = softplus(dt) if dt_softplus (x <= 20 ? log(1+e^x) : x)
  *   h' = h * exp(A * dt) + (B * dt) * x  (fp32, one fma per element, stored back with RNE)

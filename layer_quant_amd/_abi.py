@@ -67,6 +67,7 @@ EXPORTED_SYMBOLS = (
     "lq_mx_encode",
     "lq_mx_decode",
     "lq_mx_state_update",
+    "lq_mx_state_update_device_step",
     "lq_selective_state_update",
 )
 
@@ -131,6 +132,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.lq_mx_state_update.restype = ctypes.c_int
     lib.lq_mx_state_update.argtypes = [_P] * 12 + [
         ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_uint64, ctypes.c_uint64,
+        ctypes.c_void_p]
+    lib.lq_mx_state_update_device_step.restype = ctypes.c_int
+    lib.lq_mx_state_update_device_step.argtypes = [_P] * 12 + [
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_uint64, ctypes.c_uint64, _P,
         ctypes.c_void_p]
     lib.lq_selective_state_update.restype = ctypes.c_int
     lib.lq_selective_state_update.argtypes = [_P] * 10 + [ctypes.c_int, ctypes.c_void_p]
@@ -380,15 +385,24 @@ def mx_decode(q_state: torch.Tensor, shared_exp: torch.Tensor, micro_exp: torch.
 def mx_state_update(q_state, shared_exp, micro_exp, x, dt, dt_bias, A, B, C, D, z, out,
                     format_bits: int, dt_softplus: bool, round_mode: int,
                     uniform: torch.Tensor | None = None, seed: int = 1234,
-                    rng_offset: int = 0) -> torch.Tensor:
+                    rng_offset: int = 0, step: torch.Tensor | None = None) -> torch.Tensor:
+    """The fused MX update in place. With `step` (an int64 [1] tensor on the device) the counter
+    offset is rng_offset + step * B*H*P*N, read by the kernel (lq_mx_state_update_device_step):
+    graph-capturable, with the caller advancing `step`."""
     dev = _require_gpu(q_state, shared_exp, micro_exp, x, dt, dt_bias, A, B, C, D, z, out,
-                       uniform)
-    rc = lib().lq_mx_state_update(
-        desc(q_state), desc(shared_exp), desc(micro_exp), desc(x), desc(dt), desc(dt_bias),
-        desc(A), desc(B), desc(C), desc(D), desc(z), desc(out), int(format_bits),
-        1 if dt_softplus else 0, int(round_mode), desc(uniform), int(seed) & ((1 << 64) - 1),
-        int(rng_offset), _stream(dev))
-    check(rc, "lq_mx_state_update")
+                       uniform, step)
+    args = (desc(q_state), desc(shared_exp), desc(micro_exp), desc(x), desc(dt), desc(dt_bias),
+            desc(A), desc(B), desc(C), desc(D), desc(z), desc(out), int(format_bits),
+            1 if dt_softplus else 0, int(round_mode), desc(uniform), int(seed) & ((1 << 64) - 1),
+            int(rng_offset))
+    if step is None:
+        rc = lib().lq_mx_state_update(*args, _stream(dev))
+        check(rc, "lq_mx_state_update")
+    else:
+        if step.dtype != torch.int64 or step.numel() < 1:
+            raise ValueError("step must be an int64 tensor holding one value")
+        rc = lib().lq_mx_state_update_device_step(*args, desc(step.view(-1)[:1]), _stream(dev))
+        check(rc, "lq_mx_state_update_device_step")
     return out
 
 

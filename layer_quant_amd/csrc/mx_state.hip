@@ -47,9 +47,13 @@ struct MxUpdateParams {
   int has_dtb, has_D, has_z, softplus, a_row_const;
   uint32_t key;
   uint64_t rng_offset;
-  // rows kernel, counter mode: hash of the pair counters' common high word, and the low word of
-  // rng_offset / 2 (the launch's pair counters share one high word)
-  uint32_t kh, lo_base;
+  // counter mode: an optional step on the device (int64 [1]) and its stride B*H*P*N; the counter
+  // offset is rng_offset + step * stride (the reference's step*B*H*P*N, the step read by the
+  // kernel, so that a captured graph advancing it between replays draws anew on every replay)
+  const int64_t* step_dev;
+  uint64_t step_stride;
+  // rows kernel, counter mode without a device step: the counter base (below), from the host
+  uint32_t kh, kh1, lo_base;
   // rows kernel: byte stride between rows of x, z and out, and the byte span of one
   // (batch, head) slice of each rounded up to 4 (0 for an absent z)
   uint32_t x_row_bytes, z_row_bytes, out_row_bytes;
@@ -149,6 +153,26 @@ __device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
   x *= 0x846ca68bu;
   x ^= x >> 16;
   return x;
+}
+
+// Counter offset of an update: rng_offset plus, when the step lives on the device, step * stride.
+__device__ __forceinline__ uint64_t counter_offset(const MxUpdateParams& p) {
+  return p.step_dev == nullptr ? p.rng_offset
+                               : p.rng_offset + (uint64_t)(*p.step_dev) * p.step_stride;
+}
+
+// The row kernel's counter base: the low word of offset / 2 (the first pair counter) and the
+// hashes K_hi = lowbias32(hi ^ key) of its high word hi and of hi + 1 (a launch's pair counters
+// span fewer than 2^31 values, so they cross at most one high-word boundary).
+struct CounterBase {
+  uint32_t lo_base, kh, kh1;
+};
+
+__device__ __forceinline__ CounterBase counter_base(const MxUpdateParams& p) {
+  if (p.step_dev == nullptr) return CounterBase{p.lo_base, p.kh, p.kh1};
+  const uint64_t pair0 = counter_offset(p) >> 1;
+  const uint32_t hi = (uint32_t)(pair0 >> 32);
+  return CounterBase{(uint32_t)pair0, lowbias32(hi ^ p.key), lowbias32((hi + 1u) ^ p.key)};
 }
 
 // ceil(log2(t)) with log2 correctly rounded to fp32, for positive normal t (or +inf).
@@ -629,7 +653,7 @@ __global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
   // writeback encode (ms.py:168-222, 512-544)
   const uint64_t row = ((uint64_t)b * p.H + h) * p.P + pp;
   uint32_t eo_bits;
-  encode_block<FB, RMODE, LY>(hv, p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0,
+  encode_block<FB, RMODE, LY>(hv, p.uni, p.key, counter_offset(p) + row * (uint64_t)p.N + (uint64_t)n0,
                               b, h, pp, n0, qw, mw, eo_bits);
   if (L.active) store_block<VEC, LY>(qp, mp, ep, qw, mw, eo_bits);
 }
@@ -728,7 +752,8 @@ template <int FB, int RMODE, int BPR_LOG2, int R, int SLOTS, int LY>
 __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadBufs& hb, int b,
                                             int h, int row0, int slot, int blk,
                                             const RowLoads<R>& L, const float* bdp,
-                                            const float* cvp, const HeadScalars& hs) {
+                                            const float* cvp, const HeadScalars& hs,
+                                            const CounterBase& cb) {
   constexpr uint32_t N = 16u << BPR_LOG2;
   const uint32_t n0 = (uint32_t)blk * 16u;
   const int P = p.P;
@@ -799,7 +824,8 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
     uint32_t qo[4], mo[2], eo;
     if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
       const uint32_t idx = ((uint32_t)((b * p.H + h) * P + pp) * N + n0) >> 1;
-      uint32_t base = (p.lo_base + idx) ^ p.kh;
+      const uint32_t lo = cb.lo_base + idx;  // the block's first pair counter, low word
+      uint32_t base = lo ^ (lo < cb.lo_base ? cb.kh1 : cb.kh);  // its high word carried past hi
       base ^= base >> 16;
       encode16_dither<FB, LY>(hv, HashWords{base}, qo, mo, eo);
     } else {
@@ -891,8 +917,10 @@ void mx_update_rows_kernel(MxUpdateParams p) {
   hs.dt = 0.0f;  // folded into B * dt
   hs.dA = s_hs[0];
   hs.D = s_hs[1];
+  CounterBase cb{};
+  if constexpr (RMODE == LQ_ROUND_SR_COUNTER) cb = counter_base(p);
   update_rows<FB, RMODE, BPR_LOG2, R, SLOTS, LY>(p, hb, b, h, row0, slot, blk, L, &s_bd[n0],
-                                                 &s_c[n0], hs);
+                                                 &s_c[n0], hs, cb);
 }
 
 template <int FB, int RMODE, bool VEC, int LY>
@@ -1206,8 +1234,9 @@ static void dispatch_rows(const MxUpdateParams& p, int rmode, dim3 grid, hipStre
 
 // The rows kernel's preconditions (else the general kernel runs): d_state 64, 128 or 256;
 // vector-aligned state with contiguous rows; bf16 B/C with contiguous d_state; dt, dt_bias, A, D
-// constant within a head; in the counter mode rng_offset a multiple of 16 and all pair counters
-// of the launch sharing one high word, with fewer than 2^32 state elements.
+// constant within a head; in the counter mode rng_offset a multiple of 16 (then so is every
+// offset with a device step, whose stride B*H*P*N is a multiple of 16) and fewer than 2^32 state
+// elements.
 static bool rows_path_ok(const MxUpdateParams& p, bool vec, bool bcvec, const lq_tensor* dt,
                          const lq_tensor* dt_bias, const lq_tensor* A, const lq_tensor* D,
                          int round_mode, int64_t total, int layout) {
@@ -1235,9 +1264,6 @@ static bool rows_path_ok(const MxUpdateParams& p, bool vec, bool bcvec, const lq
   }
   if (round_mode == LQ_ROUND_SR_COUNTER) {
     if (p.rng_offset % 16 != 0 || total >= ((int64_t)1 << 32)) return false;
-    const uint64_t first = p.rng_offset >> 1;
-    const uint64_t last = (p.rng_offset + (uint64_t)total - 1) >> 1;
-    if ((first >> 32) != (last >> 32) || last < first) return false;
   }
   return true;
 }
@@ -1259,14 +1285,13 @@ static int grid_for(int64_t Bn, int64_t H, int64_t P, int vbpr_log2, dim3& grid)
 
 using namespace lq;
 
-extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* shared_exp,
-                                  const lq_tensor* micro_exp, const lq_tensor* x,
-                                  const lq_tensor* dt, const lq_tensor* dt_bias,
-                                  const lq_tensor* A, const lq_tensor* B, const lq_tensor* C,
-                                  const lq_tensor* D, const lq_tensor* z, const lq_tensor* out,
-                                  int format_bits, int dt_softplus, int round_mode,
-                                  const lq_tensor* uniform, uint64_t seed, uint64_t rng_offset,
-                                  void* stream) {
+static int mx_state_update(const lq_tensor* q_state, const lq_tensor* shared_exp,
+                           const lq_tensor* micro_exp, const lq_tensor* x, const lq_tensor* dt,
+                           const lq_tensor* dt_bias, const lq_tensor* A, const lq_tensor* B,
+                           const lq_tensor* C, const lq_tensor* D, const lq_tensor* z,
+                           const lq_tensor* out, int format_bits, int dt_softplus, int round_mode,
+                           const lq_tensor* uniform, uint64_t seed, uint64_t rng_offset,
+                           const lq_tensor* step, void* stream) {
   int rc;
   int64_t Bn, H, P, N;
   MxState st{};
@@ -1305,6 +1330,11 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
   if ((rc = check_round(format_bits, round_mode, uniform, Bn, H, P, N, rng_offset)) != LQ_OK) {
     return rc;
   }
+  if (step != nullptr) {
+    if ((rc = check_tensor(step, "step", 1, false, LQ_I64)) != LQ_OK) return rc;
+    if (step->shape[0] < 1) return fail(LQ_ERR_INVALID_ARG, "step must hold one value");
+    if (((uintptr_t)step->data & 7) != 0) return fail(LQ_ERR_INVALID_ARG, "step must be 8-byte aligned");
+  }
   if (Bn == 0 || H == 0 || P == 0) return LQ_OK;
 
   MxUpdateParams p{};
@@ -1333,6 +1363,10 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
   p.a_row_const = A->stride[2] == 0;
   p.key = seed_key(seed);
   p.rng_offset = rng_offset;
+  if (step != nullptr && round_mode == LQ_ROUND_SR_COUNTER) {
+    p.step_dev = (const int64_t*)step->data;
+    p.step_stride = (uint64_t)(Bn * H * P * N);
+  }
 
   const lq_tensor* spans[] = {q_state, shared_exp, micro_exp, x, dt, B, C, z, out, uniform};
   for (const lq_tensor* t : spans) {
@@ -1352,6 +1386,7 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
   if (rows_path_ok(p, vec, bcvec, dt, dt_bias, A, D, round_mode, Bn * H * P * N, layout)) {
     p.lo_base = (uint32_t)(rng_offset >> 1);
     p.kh = lowbias32_host((uint32_t)(rng_offset >> 33) ^ p.key);
+    p.kh1 = lowbias32_host(((uint32_t)(rng_offset >> 33) + 1u) ^ p.key);
     // per-row byte strides and slice spans of x, z and out
     auto row_bytes = [](const View& v) { return (uint32_t)(v.s[2] * dtype_size(v.dtype)); };
     auto span = [&](const View& v) {
@@ -1404,6 +1439,32 @@ extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* sha
   }
   if (rc != LQ_OK) return rc;
   return check_launch("lq_mx_state_update");
+}
+
+extern "C" int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* shared_exp,
+                                  const lq_tensor* micro_exp, const lq_tensor* x,
+                                  const lq_tensor* dt, const lq_tensor* dt_bias,
+                                  const lq_tensor* A, const lq_tensor* B, const lq_tensor* C,
+                                  const lq_tensor* D, const lq_tensor* z, const lq_tensor* out,
+                                  int format_bits, int dt_softplus, int round_mode,
+                                  const lq_tensor* uniform, uint64_t seed, uint64_t rng_offset,
+                                  void* stream) {
+  return mx_state_update(q_state, shared_exp, micro_exp, x, dt, dt_bias, A, B, C, D, z, out,
+                         format_bits, dt_softplus, round_mode, uniform, seed, rng_offset, nullptr,
+                         stream);
+}
+
+extern "C" int lq_mx_state_update_device_step(
+    const lq_tensor* q_state, const lq_tensor* shared_exp, const lq_tensor* micro_exp,
+    const lq_tensor* x, const lq_tensor* dt, const lq_tensor* dt_bias, const lq_tensor* A,
+    const lq_tensor* B, const lq_tensor* C, const lq_tensor* D, const lq_tensor* z,
+    const lq_tensor* out, int format_bits, int dt_softplus, int round_mode,
+    const lq_tensor* uniform, uint64_t seed, uint64_t rng_offset, const lq_tensor* step,
+    void* stream) {
+  if (step == nullptr) return fail(LQ_ERR_INVALID_ARG, "step: descriptor is NULL");
+  return mx_state_update(q_state, shared_exp, micro_exp, x, dt, dt_bias, A, B, C, D, z, out,
+                         format_bits, dt_softplus, round_mode, uniform, seed, rng_offset, step,
+                         stream);
 }
 
 extern "C" int lq_mx_encode(const lq_tensor* state, const lq_tensor* q_state,

@@ -50,6 +50,10 @@ class MambaStateKernelCache:
     format_bits: int = 8
     step: int = 0
     layout: str = "reference"
+    # optional step counter on the device (int64 [1], see enable_device_step): the counter
+    # rounding then reads it in the kernel and advances it with a tensor add, so a decode step
+    # captured in a graph draws anew on every replay
+    device_step: torch.Tensor | None = None
 
     @property
     def state_shape(self) -> tuple[int, ...]:
@@ -222,14 +226,28 @@ def mx_state_selective_update(cache: MambaStateKernelCache, x: torch.Tensor, dt:
         mode = _abi.ROUND_SR_UNIFORM
     else:
         mode = _abi.ROUND_SR_COUNTER
-    rng_offset = cache.step * batch * nheads * dim * dstate
+    on_device = cache.device_step is not None and mode == _abi.ROUND_SR_COUNTER
+    rng_offset = 0 if on_device else cache.step * batch * nheads * dim * dstate
     _abi.mx_state_update(cache.q_state, cache.shared_exp, cache.micro_exp, x, dt,
                          _dt_bias_as_read(dt_bias, D, nheads, dim), A, B, C, D, z, out,
                          cache.format_bits, dt_softplus, mode,
                          uniform=uniform if mode == _abi.ROUND_SR_UNIFORM else None,
-                         seed=seed, rng_offset=rng_offset)
+                         seed=seed, rng_offset=rng_offset,
+                         step=cache.device_step if on_device else None)
+    if cache.device_step is not None:
+        cache.device_step.add_(1)
     cache.step += 1
     return out
+
+
+def enable_device_step(cache: MambaStateKernelCache) -> MambaStateKernelCache:
+    """Keep the cache's stochastic-rounding step counter on the device as well (int64 [1],
+    starting at cache.step): the counter-mode update then takes its offset step * B*H*P*N from
+    that tensor in the kernel and advances it with a tensor add, which a captured HIP graph
+    replays, so every replay rounds with fresh draws. cache.step still counts the host-side
+    calls. No counterpart in the reference (a host integer there, ms.py:659, 716)."""
+    cache.device_step = torch.tensor([cache.step], dtype=torch.int64, device=cache.q_state.device)
+    return cache
 
 
 def mx8_state_selective_update(*args, **kwargs) -> torch.Tensor:

@@ -117,3 +117,66 @@ def test_decode_step_graph_replays_match_eager(gpu, mode):
         junk = junk * 1.0001 + 1.0  # eager work between replays
         torch.cuda.synchronize()
     assert torch.isfinite(t["att"]).all()
+
+
+@pytest.mark.parametrize("path", ["rows", "general"])
+def test_device_step_graph_replays_draw_anew(gpu, diag, path):
+    """An MX4 counter-mode update through the module with its step counter on the device
+    (enable_device_step), captured together with the step's advance and replayed three times:
+    the states are bit-identical to three eager host-offset updates at offsets 0, T and 2T
+    (T = B*H*P*N), i.e. fresh draws on every replay, not three copies of one step's."""
+    from hybrid_quant import mamba_state_8b_kernel as ms
+
+    diag.set("LQ_MX_REQUIRE_ROWS" if path == "rows" else "LQ_MX_FORCE_GENERIC")
+    t = _make_state(gpu, 99)
+    bsz, nh, p_, n = t["st"][0].shape
+    T = bsz * nh * p_ * n
+    start = [a.clone() for a in t["st"]]
+
+    def eager(offsets):
+        st = [a.clone() for a in start]
+        snaps = []
+        for off in offsets:
+            _abi.mx_state_update(*st, t["x"], t["dt"], t["dt_bias"], t["A"], t["B"], t["C"],
+                                 t["D"], None, t["y"], 4, True, _abi.ROUND_SR_COUNTER,
+                                 seed=1234, rng_offset=off)
+            torch.cuda.synchronize()
+            snaps.append([a.clone() for a in st])
+        return snaps
+
+    want = eager([0, T, 2 * T])
+    frozen = eager([0, 0, 0])
+    assert not all(torch.equal(a, b) for a, b in zip(want[2], frozen[2]))  # offsets matter
+
+    cache = ms.MambaStateKernelCache(*[a.clone() for a in start], format_bits=4)
+    ms.enable_device_step(cache)
+
+    def step():
+        # dt_bias as the module reads it (with D's strides, ms.py:137): the same tensor here
+        return ms.mx_state_selective_update(cache, t["x"], t["dt"], t["A"], t["B"], t["C"],
+                                            D=t["D"], dt_bias=t["dt_bias"], dt_softplus=True)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()  # warm-up (advances the step; reset below)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    for dst, src in zip((cache.q_state, cache.shared_exp, cache.micro_exp), start):
+        dst.copy_(src)
+    cache.device_step.fill_(0)
+    torch.cuda.synchronize()
+    junk = torch.randn(1 << 20, device=gpu)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (cache.q_state, cache.shared_exp, cache.micro_exp)
+        for a, b in zip(got, want[i]):
+            assert torch.equal(a, b), f"replay {i}"
+        assert int(cache.device_step.item()) == i + 1
+        junk = junk * 1.0001 + 1.0  # eager work between replays
+        torch.cuda.synchronize()

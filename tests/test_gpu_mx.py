@@ -368,3 +368,34 @@ def test_config3_batch1_full_layer_every_group(gpu, diag, fb, mode):
     mag = update_term_magnitudes(omx.mx_decode(q0, e0, m0), *args)
     assert_mx_writeback([a.cpu().numpy() for a in st], (rq, re_, rm), rh, mag, fb, mode,
                         uniform=uni, seed=seed, rng_offset=off, what=f"state mx{fb} mode {mode}")
+
+
+@pytest.mark.parametrize("fb", [4, 8])
+def test_counter_offsets_crossing_a_high_word_row_kernel(gpu, diag, fb):
+    """Counter offsets whose pair counters cross a 2^32 boundary of their high word inside one
+    launch (the row kernel switches the per-block hash of the high word where the low word
+    carries): the dt = 0 writeback is bit-exact against the oracle, through the host offset and
+    through a device step (lq_mx_state_update_device_step) giving the same offset."""
+    diag.set("LQ_MX_REQUIRE_ROWS")
+    shape = (2, 4, 16, 128)
+    T = int(np.prod(shape))
+    h0 = _state(shape, 500 + fb)
+    t = _inputs(2, 4, 16, 128, 2, 501, gpu, dt_zero=True, head_dt=True)
+    st0 = _mx_tensors(shape, gpu)
+    _abi.mx_encode(h0.to(gpu), *st0, fb, 0)
+    q0, e0, m0 = (a.cpu().numpy() for a in st0)
+    base = (1 << 33) - T // 2 - 5 * T  # at step 5 the pair counters run from 2^32 - T/4 over 2^32
+    step = torch.tensor([5], dtype=torch.int64, device=gpu)
+    for how in ("host", "device"):
+        st = [a.clone() for a in st0]
+        out = torch.empty(2, 4, 16, device=gpu)
+        if how == "host":
+            _abi.mx_state_update(*st, t["x"], t["dt"], None, t["A"], t["B"], t["C"], None, None,
+                                 out, fb, False, 3, seed=77, rng_offset=base + 5 * T)
+        else:
+            _abi.mx_state_update(*st, t["x"], t["dt"], None, t["A"], t["B"], t["C"], None, None,
+                                 out, fb, False, 3, seed=77, rng_offset=base, step=step)
+        torch.cuda.synchronize()
+        ref = omx.mx_encode(omx.mx_decode(q0, e0, m0), fb, omx.ROUND_SR_COUNTER, seed=77,
+                            rng_offset=base + 5 * T)
+        _assert_mx_equal(st, ref)
