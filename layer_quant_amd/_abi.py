@@ -38,7 +38,7 @@ DIAG_BITS = {
     "LQ_MX_REQUIRE_ROWS": 1 << 5,
     "LQ_SSM_FORCE_GENERIC": 1 << 6,
     "LQ_SSM_REQUIRE_ROWS": 1 << 7,
-    "LQ_ATTN_MERGE_KERNEL": 1 << 8,
+    "LQ_ATTN_FOLD_MERGE": 1 << 8,
 }
 
 DTYPE_CODES = {

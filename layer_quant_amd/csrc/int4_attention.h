@@ -22,7 +22,7 @@ struct AttnParams {
   float* ws_l;
   float* ws_acc;
   uint32_t* ws_cnt;  // arrival counters of the (batch, KV head) units (fold)
-  int fold;          // the fast kernel merges its own splits (no attn_merge_kernel launch)
+  int fold;          // the fast kernel merges its own splits (LQ_DIAG_ATTN_FOLD_MERGE)
   int B, Hq, Hkv, D, g, nrep;
   int64_t S;
   int nsplit;     // workgroup splits along the keys

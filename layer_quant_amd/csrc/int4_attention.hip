@@ -8,9 +8,10 @@
 //     (batch, query head, split), fp32 VALU throughout.
 // Scores follow the reference: s_n = (q . k_n) * log2(e)/sqrt(D) (+ mask_n), exp2-domain online
 // softmax; keys at or beyond the mask length get -inf. Splits write (m, l, acc[D]) partials into
-// the caller's workspace; the MFMA kernel's last workgroup of each (batch, KV head) merges them
-// (counted by arrival counters at the start of the workspace), otherwise attn_merge_kernel does;
-// a single split writes out directly.
+// the caller's workspace and attn_merge_kernel merges them; a single split writes out directly.
+// With LQ_DIAG_ATTN_FOLD_MERGE the MFMA kernel's last workgroup of each (batch, KV head) merges
+// them instead (counted by arrival counters at the start of the workspace): one launch, but
+// slower at every measured shape, the kernel growing by more than the merge launch takes.
 // lq_int4_decode_attention_pack first packs the new token into cache row seq_len - 1 (the
 // reference's _pack_kv_into_cache at :477-515): inside attn_fast_kernel on the MFMA path, by the
 // pack kernel before the generic one otherwise.
@@ -523,9 +524,9 @@ static int decode_attention(const lq_tensor* q, const lq_tensor* k_packed,
       return rc;
     }
   }
-  // the MFMA kernel merges its own splits when the unit count fits the arrival counters
+  // on request, the MFMA kernel merges its own splits when the unit count fits the counters
   p.fold = fast && p.nsplit > 1 && B * Hkv <= ARRIVAL_UNITS &&
-           fast_fold_fits(num_key_value_groups, p.nsplit) && !diag(LQ_DIAG_ATTN_MERGE_KERNEL);
+           fast_fold_fits(num_key_value_groups, p.nsplit) && diag(LQ_DIAG_ATTN_FOLD_MERGE);
   if (fast) {
     if ((rc = launch_fast(p, st)) != LQ_OK) return rc;
   } else {

@@ -250,17 +250,19 @@ __device__ __forceinline__ float coherent_load(const float* a) {
 }
 
 // The folded merge handles units with NREP * nsplit <= FOLD_MAX_PARTIALS: one thread's outputs
-// then need at most FOLD_MAX_PARTIALS / 2 partial loads, all issued at once.
+// then need at most 64 partial loads (128 at NREP = 1), all issued at once.
 constexpr int FOLD_MAX_PARTIALS = 128;
 
 // The merge of one (batch, KV head) unit's nsplit partials, by the unit's workgroup that arrived
-// last: every load goes out at once (thread t's acc partials of outputs t + 256 j over all
-// splits, and one (m, l) pair per thread for the first NREP * nsplit threads, through LDS), so
-// the merge costs one round trip of device-coherent loads. The same formulas as
-// attn_merge_kernel: M = max_s m_s, w_s = 2^(m_s - M), out = sum_s w_s acc_s / sum_s w_s l_s.
+// last, with the formulas of attn_merge_kernel: M = max_s m_s, w_s = 2^(m_s - M),
+// out = sum_s w_s acc_s / sum_s w_s l_s. Every load goes out at once (thread t's acc partials of
+// outputs t + 256 j over all splits; one (m, l) pair per thread for the first NREP * nsplit
+// threads), so the merge costs one round trip of device-coherent loads. The weights are made once
+// per (head, split) by those threads and shared through LDS, and every LDS walk over the splits is
+// unrolled: computed per output, with a loop per split, the merge took 4-9 us of the kernel.
 template <int NREP>
-__device__ __forceinline__ void merge_unit(const AttnParams& p, int b, int kvh, float* s_m,
-                                           float* s_l) {
+__device__ __forceinline__ void merge_unit(const AttnParams& p, int b, int kvh, float* s_w,
+                                           float* s_wl, float* s_L) {
   constexpr int OPT = (NREP * FAST_D + THREADS - 1) / THREADS;  // outputs per thread
   constexpr int SMAX = FOLD_MAX_PARTIALS / NREP;                // splits at most
   const int tid = threadIdx.x;
@@ -277,9 +279,41 @@ __device__ __forceinline__ void merge_unit(const AttnParams& p, int b, int kvh, 
       part[j][s] = (s < ns) ? coherent_load(&p.ws_acc[((head0 + h) * ns + s) * FAST_D + d]) : 0.0f;
     }
   }
-  if (tid < NREP * ns) {
-    s_m[tid] = coherent_load(&p.ws_m[head0 * ns + tid]);  // [h][s], h-major as in the workspace
-    s_l[tid] = coherent_load(&p.ws_l[head0 * ns + tid]);
+  // thread t < NREP * ns holds split s = t % ns of head h = t / ns ([h][s], h-major as in the
+  // workspace); entries s >= ns of a head read a neighbour's slot (below FOLD_MAX_PARTIALS) and
+  // are masked
+  const bool owner = tid < NREP * ns;
+  const int oh = owner ? tid / ns : 0;
+  float mt = -INFINITY, lt = 0.0f;
+  if (owner) {
+    mt = coherent_load(&p.ws_m[head0 * ns + tid]);
+    lt = coherent_load(&p.ws_l[head0 * ns + tid]);
+    s_w[tid] = mt;
+  }
+  __syncthreads();
+  float w = 0.0f;
+  if (owner) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      const float ms = s_w[min(oh * ns + s, FOLD_MAX_PARTIALS - 1)];
+      M = fmaxf(M, s < ns ? ms : -INFINITY);
+    }
+    w = (mt == -INFINITY) ? 0.0f : exp2f(mt - M);
+    s_wl[tid] = w * lt;
+  }
+  __syncthreads();
+  if (owner) {
+    s_w[tid] = w;  // every read of the m values ended at the barrier above
+    if (tid == oh * ns) {
+      float L = 0.0f;
+#pragma unroll
+      for (int s = 0; s < SMAX; ++s) {
+        const float wl = s_wl[min(oh * ns + s, FOLD_MAX_PARTIALS - 1)];
+        L += s < ns ? wl : 0.0f;
+      }
+      s_L[oh] = L;
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -288,21 +322,15 @@ __device__ __forceinline__ void merge_unit(const AttnParams& p, int b, int kvh, 
     if (o >= NREP * FAST_D) break;
     const int h = o / FAST_D;
     const int d = o % FAST_D;
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, s_m[h * ns + s]);
-    float L = 0.0f, a = 0.0f;
+    float a = 0.0f;
 #pragma unroll
     for (int s = 0; s < SMAX; ++s) {
-      if (s < ns) {
-        const float ms = s_m[h * ns + s];
-        const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
-        L += w * s_l[h * ns + s];
-        a += w * part[j][s];
-      }
+      const float ws = s_w[min(h * ns + s, FOLD_MAX_PARTIALS - 1)];
+      a += (s < ns ? ws : 0.0f) * part[j][s];
     }
     const int qh = kvh * NREP + h;
     store_float(p.out.data, p.out.dtype, b * p.out.s[0] + qh * p.out.s[1] + d * p.out.s[2],
-                a / L);
+                a / s_L[h]);
   }
 }
 
@@ -676,7 +704,7 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
     // a write-back and an invalidate of the whole L2 per workgroup) made batch 1, ctx 4096 take
     // 32.4 instead of 14.0 us.
     __shared__ int s_last;
-    __shared__ float s_m[FOLD_MAX_PARTIALS], s_l[FOLD_MAX_PARTIALS];
+    __shared__ float s_w[FOLD_MAX_PARTIALS], s_wl[FOLD_MAX_PARTIALS], s_L[16];
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
@@ -685,7 +713,7 @@ __global__ __launch_bounds__(THREADS) void attn_fast_kernel(AttnParams p) {
     }
     __syncthreads();
     if (!s_last) return;
-    merge_unit<NREP>(p, b, kvh, s_m, s_l);
+    merge_unit<NREP>(p, b, kvh, s_w, s_wl, s_L);
     if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }

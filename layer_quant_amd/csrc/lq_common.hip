@@ -68,7 +68,7 @@ int check_tensor(const lq_tensor* t, const char* name, int ndim, bool float_dtyp
 static const char* const kDiagEnv[] = {
     "LQ_ATTN_FORCE_GENERIC", "LQ_ATTN_REQUIRE_FAST", "LQ_PREFILL_FORCE_GENERIC",
     "LQ_PREFILL_REQUIRE_MFMA", "LQ_MX_FORCE_GENERIC", "LQ_MX_REQUIRE_ROWS",
-    "LQ_SSM_FORCE_GENERIC", "LQ_SSM_REQUIRE_ROWS", "LQ_ATTN_MERGE_KERNEL"};
+    "LQ_SSM_FORCE_GENERIC", "LQ_SSM_REQUIRE_ROWS", "LQ_ATTN_FOLD_MERGE"};
 
 static uint32_t diag_from_env() {
   uint32_t flags = 0;

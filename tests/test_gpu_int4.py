@@ -358,13 +358,12 @@ def test_module_api_pack_then_attend(gpu):
 
 
 def test_folded_split_merge_matches_merge_kernel_and_leaves_counters_zero(gpu, diag):
-    """Multi-split MFMA calls merge their partials in the kernel (the last workgroup of each
-    (batch, KV head) to arrive): over shapes with 2-64 splits, masked and not, groups 32/64/128,
-    1-16 query heads per KV head, all through one reused workspace, the output equals the
-    two-launch form's (LQ_ATTN_MERGE_KERNEL: the same partials, merged by attn_merge_kernel,
+    """With LQ_ATTN_FOLD_MERGE, multi-split MFMA calls merge their partials in the kernel (the
+    last workgroup of each (batch, KV head) to arrive): over shapes with 2-64 splits, masked and
+    not, groups 32/64/128, 1-16 query heads per KV head, all through one reused workspace, the
+    output equals the default two-launch form's (the same partials, merged by attn_merge_kernel,
     whose sums run in another order: within 1e-5 of the output's mean magnitude) and the
-    oracle's, and after every
-    call the workspace's arrival counters are all zero again."""
+    oracle's, and after every call the workspace's arrival counters are all zero again."""
     diag.set("LQ_ATTN_REQUIRE_FAST")
     gen = torch.Generator(device=gpu).manual_seed(77)
     d = 128
@@ -387,7 +386,7 @@ def test_folded_split_merge_matches_merge_kernel_and_leaves_counters_zero(gpu, d
             mask[..., s // 3: s // 2] = float("-inf")
         outs = []
         for merge_kernel in (False, True):
-            with _abi.diagnostic("LQ_ATTN_MERGE_KERNEL", on=merge_kernel):
+            with _abi.diagnostic("LQ_ATTN_FOLD_MERGE", on=not merge_kernel):
                 out = torch.full((b, hkv * nrep, d), float("nan"), device=gpu)
                 rc = lib.lq_int4_decode_attention(
                     _abi.desc(q), _abi.desc(kp), _abi.desc(vp), _abi.desc(ks), _abi.desc(vs),
