@@ -393,6 +393,10 @@ void prefill_mfma_kernel(PrefillParams p) {
       }
       l_run[qt] += psum;
     }
+    // Wave priority 1 over P' and the P V products: of the two waves on a SIMD, the one in this
+    // section issues first, the other's QK and softmax work filling in behind it (L = 16384:
+    // 4.47 against 4.89 ms; the same over the QK products gains nothing)
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int m = 0; m < G; ++m) {
       f32x4_t vs4[2];
@@ -425,6 +429,7 @@ void prefill_mfma_kernel(PrefillParams p) {
         for (int qt = 0; qt < 2; ++qt) o[qt][it] = mfma_f16(va, blo[qt], o[qt][it]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   }
 
   if (!active) return;
