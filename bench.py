@@ -899,6 +899,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
+        "dtype_note": ("fp32 accumulation and softmax; the attention's MFMA operands are exact "
+                       "bf16 values (queries, nibbles as offset integers) except the P V weights "
+                       "p * vscale, which enter as a bf16 hi + lo pair (about 16 significant "
+                       "bits); the MX update is fp32 VALU"),
         "data": "synthetic",
         "config": {
             "workload": (f"Nemotron-H-8B decode step, quantized paths only: {args.attn_layers} "
