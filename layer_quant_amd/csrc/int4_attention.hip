@@ -10,8 +10,8 @@
 // softmax; keys at or beyond the mask length get -inf. Splits write (m, l, acc[D]) partials into
 // the caller's workspace and attn_merge_kernel merges them; a single split writes out directly.
 // With LQ_DIAG_ATTN_FOLD_MERGE the MFMA kernel's last workgroup of each (batch, KV head) merges
-// them instead (counted by arrival counters at the start of the workspace): one launch, but
-// slower at every measured shape, the kernel growing by more than the merge launch takes.
+// them instead (counted by arrival counters at the start of the workspace): one launch, but at
+// batch 1 the kernel grows by more than the merge launch takes.
 // lq_int4_decode_attention_pack first packs the new token into cache row seq_len - 1 (the
 // reference's _pack_kv_into_cache at :477-515): inside attn_fast_kernel on the MFMA path, by the
 // pack kernel before the generic one otherwise.
