@@ -360,7 +360,8 @@ def test_module_api_pack_then_attend(gpu):
 def test_folded_split_merge_matches_merge_kernel_and_leaves_counters_zero(gpu, diag):
     """With LQ_ATTN_FOLD_MERGE, multi-split MFMA calls merge their partials in the kernel (the
     last workgroup of each (batch, KV head) to arrive): over shapes with 2-64 splits, masked and
-    not, groups 32/64/128, 1-16 query heads per KV head, all through one reused workspace, the
+    not, groups 32/64/128, 1-16 query heads per KV head (1 head: 128 splits' partials per thread in
+    the merge), all through one reused workspace, the
     output equals the default two-launch form's (the same partials, merged by attn_merge_kernel,
     whose sums run in another order: within 1e-5 of the output's mean magnitude) and the
     oracle's, and after every call the workspace's arrival counters are all zero again."""
@@ -371,7 +372,8 @@ def test_folded_split_merge_matches_merge_kernel_and_leaves_counters_zero(gpu, d
     ws = torch.zeros(4 << 20, dtype=torch.uint8, device=gpu)
     lib = _abi.lib()
     cases = [(1, 8, 4, 16384, 32, False), (8, 8, 4, 2072, 64, False), (2, 8, 4, 5000, 32, True),
-             (1, 1, 16, 9000, 128, False), (3, 2, 8, 3001, 64, True), (1, 8, 2, 700, 32, False)]
+             (1, 1, 16, 9000, 128, False), (3, 2, 8, 3001, 64, True), (1, 8, 2, 700, 32, False),
+             (1, 8, 1, 16384, 32, False), (2, 4, 1, 4100, 64, True)]
     for b, hkv, nrep, s, g, masked in cases:
         need = lib.lq_int4_decode_attention_workspace(b, hkv * nrep, hkv, d, s, g)
         assert need > 64 << 10, (b, s, need)  # several splits
