@@ -457,6 +457,16 @@ def sweep(torch, dev, args):
                 B, nh, p_, n, ng, format_bits=bits) + 4 * uni.numel(), med, mean, batch=B,
                 layout="reference", rounding="stochastic (supplied uniform tensor)"))
         del uni
+        # the reference's own draws (tl.rand's Philox4x32-10 per element, generated in the kernel)
+        for bits in (8, 4):
+            st = _mx_tensors(torch, (B, nh, p_, n), bits, "reference", dev)
+            _abi.mx_encode(h0, *st, bits, _abi.ROUND_NEAREST_EVEN)
+            med, mean = timed(lambda: _abi.mx_state_update(*st, x, dt, dtb, A, Bm, Cm, D, None, out,
+                                                           bits, True, _abi.ROUND_SR_PHILOX,
+                                                           seed=1234))
+            rows.append(row(f"mx{bits}_state_update", mx_update_bytes(
+                B, nh, p_, n, ng, format_bits=bits), med, mean, batch=B, layout="reference",
+                rounding="stochastic (Philox, the reference's tl.rand stream)"))
         state = h0.to(torch.bfloat16)
         med, mean = timed(lambda: _abi.selective_state_update(state, x, dt, dtb, A, Bm, Cm, D, None,
                                                               out, True))

@@ -58,8 +58,10 @@ enum {
   LQ_ROUND_NEAREST_EVEN = 0, /* torch.round of clamp(|v|/scale, 0, M): the initial encode       */
   LQ_ROUND_HALF_UP = 1,      /* floor(min(|v|/scale, M) + 0.5): the deterministic writeback     */
   LQ_ROUND_SR_UNIFORM = 2,   /* floor(q) + (u < q - floor(q)), u from a caller fp32 tensor       */
-  LQ_ROUND_SR_COUNTER = 3    /* stochastic, 16-bit draws of the library's counter generator:    */
+  LQ_ROUND_SR_COUNTER = 3,   /* stochastic, 16-bit draws of the library's counter generator:    */
                              /* floor(RN_{2^-16}(v/scale + u)), u = u16 * 2^-16 (see below)     */
+  LQ_ROUND_SR_PHILOX = 4     /* floor(q) + (u < q - floor(q)), u = the reference's own draw     */
+                             /* tl.rand(seed, offset): Triton's Philox4x32-10 (see below)      */
 };
 /*
  * The counter-based generator of LQ_ROUND_SR_COUNTER: element (b,h,p,n) draws counter
@@ -71,6 +73,18 @@ enum {
  * the draw rounded to the 2^-16 grid (ties to even), floored, so |v| rounds up with probability
  * round(frac(|qs|) * 2^16) / 2^16 (bias within 2^-17 of a level step).
  * lowbias32(x): x ^= x>>16; x *= 0x7feb352d; x ^= x>>15; x *= 0x846ca68b; x ^= x>>16.
+ *
+ * LQ_ROUND_SR_PHILOX reproduces the reference's stochastic writeback, u = tl.rand(RNG_SEED,
+ * RNG_OFFSET + index) (hybrid_quant/mamba_state_8b_kernel.py:198, 405, 479, 529; Triton's
+ * triton/language/random.py), bit for bit: element (b,h,p,n) takes offset
+ * c = rng_offset + ((b*H + h)*P + p)*N + n and runs Philox4x32 with 10 rounds on the counter
+ * (lo32(c), hi32(c), 0, 0) under the key (lo32(seed), hi32(seed)):
+ *   c0' = mulhi(0xCD9E8D57, c2) ^ c1 ^ k0;  c1' = 0xCD9E8D57 * c2;
+ *   c2' = mulhi(0xD2511F53, c0) ^ c3 ^ k1;  c3' = 0xD2511F53 * c0;  k0 += 0x9E3779B9;
+ *   k1 += 0xBB67AE85.  With x = (int32) c0 after the last round, u = fp32(x < 0 ? -x-1 : x) *
+ *   0x1.fffffep-32 in [0, 1 - 2^-24]. The level is floor(q) + (u < q - floor(q)), as in
+ *   LQ_ROUND_SR_UNIFORM. (The reference's offsets are int32: they agree with c wherever its
+ *   kernels compile.) About 4x the arithmetic of the counter mode: a fidelity mode.
  */
 
 typedef struct lq_tensor {
@@ -252,8 +266,8 @@ int lq_int4_prefill_attention(const lq_tensor* q, const lq_tensor* k_packed,
  * _quantize_initial_state_mx (reference hybrid_quant/mamba_state_8b_kernel.py:547-572); the
  * other modes run the writeback encoder of :168-222 / :494-544 on a given state.
  *   uniform    [B,H,P,N] f32, required for LQ_ROUND_SR_UNIFORM, else NULL
- *   seed, rng_offset: counter of LQ_ROUND_SR_COUNTER (element (b,h,p,n) draws counter
- *   rng_offset + ((b*H + h)*P + p)*N + n)
+ *   seed, rng_offset: counter of LQ_ROUND_SR_COUNTER and LQ_ROUND_SR_PHILOX (element (b,h,p,n)
+ *   draws counter rng_offset + ((b*H + h)*P + p)*N + n)
  */
 int lq_mx_encode(const lq_tensor* state, const lq_tensor* q_state, const lq_tensor* shared_exp,
                  const lq_tensor* micro_exp, int format_bits, int round_mode,
@@ -290,8 +304,9 @@ int lq_mx_state_update(const lq_tensor* q_state, const lq_tensor* shared_exp,
 
 /*
  * lq_mx_state_update with the counter offset's step on the device: the same arguments and
- * results, with LQ_ROUND_SR_COUNTER's offset rng_offset + step[0] * B*H*P*N, where step is an
- * int64 [1] tensor on the device that the kernel reads when it runs (the reference's offsets
+ * results, with LQ_ROUND_SR_COUNTER's and LQ_ROUND_SR_PHILOX's offset
+ * rng_offset + step[0] * B*H*P*N, where step is an int64 [1] tensor on the device that the
+ * kernel reads when it runs (the reference's offsets
  * step*B*H*P*N with the step counter on the device; other rounding modes ignore it). A caller that
  * captures an update in a HIP graph and advances step inside the graph (e.g. a captured add of 1)
  * draws fresh values on every replay; with the host offset the draws of the capture would repeat.

@@ -27,6 +27,7 @@ ROUND_NEAREST_EVEN = 0
 ROUND_HALF_UP = 1
 ROUND_SR_UNIFORM = 2
 ROUND_SR_COUNTER = 3
+ROUND_SR_PHILOX = 4
 
 # LQ_DIAG_* bits of the library's diagnostic switches, by their environment-variable names
 DIAG_BITS = {

@@ -23,6 +23,8 @@
 //   level = rint(qa) | floor(qa + 0.5) | floor(qa) + (u < qa - floor(qa))   (always <= M)
 // The counter mode (LQ_ROUND_SR_COUNTER) draws 16-bit integers u16 and dithers on a 2^-16 grid:
 //   t = RN(v / (base*2^micro) + 192 + u16 * 2^-16)  (one fma),  level = floor(t) - 192
+// The Philox mode (LQ_ROUND_SR_PHILOX) draws the reference's own u = tl.rand(seed, offset) per
+// element (Philox4x32-10, philox_uniform below) and applies the supplied-uniform formula.
 #include <math.h>
 #include <stdlib.h>
 
@@ -46,8 +48,9 @@ struct MxUpdateParams {
   int Bn, H, P, N, ratio, bpr, vbpr_log2;
   int has_dtb, has_D, has_z, softplus, a_row_const;
   uint32_t key;
+  uint32_t pk0, pk1;  // Philox mode: the key words lo32(seed), hi32(seed)
   uint64_t rng_offset;
-  // counter mode: an optional step on the device (int64 [1]) and its stride B*H*P*N; the counter
+  // counter and Philox modes: an optional step on the device (int64 [1]) and its stride B*H*P*N; the counter
   // offset is rng_offset + step * stride (the reference's step*B*H*P*N, the step read by the
   // kernel, so that a captured graph advancing it between replays draws anew on every replay)
   const int64_t* step_dev;
@@ -69,6 +72,7 @@ struct MxCodecParams {
   View uni;  // uniforms for LQ_ROUND_SR_UNIFORM
   int Bn, H, P, N, bpr, vbpr_log2;
   uint32_t key;
+  uint32_t pk0, pk1;  // Philox mode: the key words lo32(seed), hi32(seed)
   uint64_t rng_offset;
 };
 
@@ -153,6 +157,36 @@ __device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
   x *= 0x846ca68bu;
   x ^= x >> 16;
   return x;
+}
+
+// Triton's tl.rand(seed, c) for the 64-bit offset c (triton/language/random.py, the stream of the
+// reference's writeback, hybrid_quant/mamba_state_8b_kernel.py:198, 405, 479, 529): Philox4x32
+// with 10 rounds (Salmon et al., SC'11) of the counter (lo32(c), hi32(c), 0, 0) under the key
+// (lo32(seed), hi32(seed)); its first word x, as int32, becomes (x < 0 ? -x - 1 : x) * 0x1.fffffep-32
+// in fp32. The key schedule is the same for every lane (scalar registers).
+__device__ __forceinline__ float philox_uniform(uint32_t k0, uint32_t k1, uint64_t c) {
+  constexpr uint32_t RA = 0xD2511F53u, RB = 0xCD9E8D57u, KA = 0x9E3779B9u, KB = 0xBB67AE85u;
+  uint32_t c0 = (uint32_t)c, c1 = (uint32_t)(c >> 32), c2 = 0u, c3 = 0u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t a0 = c0, a2 = c2;
+    c0 = __umulhi(RB, a2) ^ c1 ^ k0;
+    c2 = __umulhi(RA, a0) ^ c3 ^ k1;
+    c1 = RB * a2;
+    c3 = RA * a0;
+    k0 += KA;
+    k1 += KB;
+  }
+  const int32_t x = (int32_t)c0;
+  return (float)(x < 0 ? ~x : x) * 0x1.fffffep-32f;
+}
+
+// The Philox draws of one 16-value block (element i at offset c0 + i) scaled by 2^16 (exact),
+// in the form encode16 takes supplied uniforms.
+__device__ __forceinline__ void philox_block_u16(uint32_t k0, uint32_t k1, uint64_t c0,
+                                                 float (&u16)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) u16[i] = philox_uniform(k0, k1, c0 + (uint64_t)i) * 65536.0f;
 }
 
 // Counter offset of an update: rng_offset plus, when the step lives on the device, step * stride.
@@ -556,13 +590,17 @@ __device__ __forceinline__ void block_u16(const View& uni, int b, int h, int pp,
 // Writeback encode of one block in mode RMODE; c0 = counter of the block's first element.
 template <int FB, int RMODE, int LY>
 __device__ __forceinline__ void encode_block(const float (&v)[16], const View& uni, uint32_t key,
-                                             uint64_t c0, int b, int h, int pp, int n0,
-                                             uint32_t (&qw)[4], uint32_t (&mw)[2],
-                                             uint32_t& eb) {
+                                             uint32_t pk0, uint32_t pk1, uint64_t c0, int b,
+                                             int h, int pp, int n0, uint32_t (&qw)[4],
+                                             uint32_t (&mw)[2], uint32_t& eb) {
   if constexpr (RMODE == LQ_ROUND_SR_COUNTER) {
     uint32_t pw[8];
     block_words(key, c0, pw);
     encode16_dither<FB, LY>(v, ArrayWords{pw}, qw, mw, eb);
+  } else if constexpr (RMODE == LQ_ROUND_SR_PHILOX) {
+    float u16[16];
+    philox_block_u16(pk0, pk1, c0, u16);
+    encode16<FB, LQ_ROUND_SR_UNIFORM, LY>(v, u16, qw, mw, eb);
   } else {
     float u16[16];
     block_u16<RMODE>(uni, b, h, pp, n0, u16);
@@ -653,8 +691,9 @@ __global__ __launch_bounds__(256) void mx_update_kernel(MxUpdateParams p) {
   // writeback encode (ms.py:168-222, 512-544)
   const uint64_t row = ((uint64_t)b * p.H + h) * p.P + pp;
   uint32_t eo_bits;
-  encode_block<FB, RMODE, LY>(hv, p.uni, p.key, counter_offset(p) + row * (uint64_t)p.N + (uint64_t)n0,
-                              b, h, pp, n0, qw, mw, eo_bits);
+  encode_block<FB, RMODE, LY>(hv, p.uni, p.key, p.pk0, p.pk1,
+                              counter_offset(p) + row * (uint64_t)p.N + (uint64_t)n0, b, h, pp, n0,
+                              qw, mw, eo_bits);
   if (L.active) store_block<VEC, LY>(qp, mp, ep, qw, mw, eo_bits);
 }
 
@@ -753,7 +792,7 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
                                             int h, int row0, int slot, int blk,
                                             const RowLoads<R>& L, const float* bdp,
                                             const float* cvp, const HeadScalars& hs,
-                                            const CounterBase& cb) {
+                                            const CounterBase& cb, uint64_t poff) {
   constexpr uint32_t N = 16u << BPR_LOG2;
   const uint32_t n0 = (uint32_t)blk * 16u;
   const int P = p.P;
@@ -828,6 +867,11 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
       uint32_t base = lo ^ (lo < cb.lo_base ? cb.kh1 : cb.kh);  // its high word carried past hi
       base ^= base >> 16;
       encode16_dither<FB, LY>(hv, HashWords{base}, qo, mo, eo);
+    } else if constexpr (RMODE == LQ_ROUND_SR_PHILOX) {
+      float u16[16];
+      const uint64_t row = ((uint64_t)b * (uint32_t)p.H + (uint32_t)h) * (uint32_t)P + pc;
+      philox_block_u16(p.pk0, p.pk1, poff + row * N + n0, u16);
+      encode16<FB, LQ_ROUND_SR_UNIFORM, LY>(hv, u16, qo, mo, eo);
     } else {
       float u16[16];
       if constexpr (RMODE == LQ_ROUND_SR_UNIFORM) {
@@ -919,8 +963,10 @@ void mx_update_rows_kernel(MxUpdateParams p) {
   hs.D = s_hs[1];
   CounterBase cb{};
   if constexpr (RMODE == LQ_ROUND_SR_COUNTER) cb = counter_base(p);
+  uint64_t poff = 0;
+  if constexpr (RMODE == LQ_ROUND_SR_PHILOX) poff = counter_offset(p);
   update_rows<FB, RMODE, BPR_LOG2, R, SLOTS, LY>(p, hb, b, h, row0, slot, blk, L, &s_bd[n0],
-                                                 &s_c[n0], hs, cb);
+                                                 &s_c[n0], hs, cb, poff);
 }
 
 template <int FB, int RMODE, bool VEC, int LY>
@@ -936,8 +982,9 @@ __global__ __launch_bounds__(256) void mx_encode_kernel(MxCodecParams p) {
   for (int i = 0; i < 16; ++i) v[i] = ldf(vb, p.v.dtype, voff + i * (int)p.v.s[3]);
   const uint64_t row = ((uint64_t)b * p.H + h) * p.P + pp;
   uint32_t qw[4], mw[2], eb;
-  encode_block<FB, RMODE, LY>(v, p.uni, p.key, p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0,
-                              b, h, pp, n0, qw, mw, eb);
+  encode_block<FB, RMODE, LY>(v, p.uni, p.key, p.pk0, p.pk1,
+                              p.rng_offset + row * (uint64_t)p.N + (uint64_t)n0, b, h, pp, n0, qw,
+                              mw, eb);
   int8_t* qp;
   uint8_t *mp, *ep;
   block_ptrs<LY>(p.st, b, h, pp, L.blk, qp, mp, ep);
@@ -1056,7 +1103,7 @@ static int check_round(int format_bits, int round_mode, const lq_tensor* uniform
   if (format_bits != 8 && format_bits != 4) {
     return fail(LQ_ERR_INVALID_ARG, "Unsupported MX state format_bits=%d", format_bits);
   }
-  if (round_mode < LQ_ROUND_NEAREST_EVEN || round_mode > LQ_ROUND_SR_COUNTER) {
+  if (round_mode < LQ_ROUND_NEAREST_EVEN || round_mode > LQ_ROUND_SR_PHILOX) {
     return fail(LQ_ERR_INVALID_ARG, "unknown round_mode %d", round_mode);
   }
   if (round_mode == LQ_ROUND_SR_UNIFORM) {
@@ -1164,6 +1211,9 @@ static void dispatch_update(const MxUpdateParams& p, int rmode, bool vec, bool b
     case LQ_ROUND_SR_UNIFORM:
       launch_update<FB, LQ_ROUND_SR_UNIFORM, LY>(p, vec, bcvec, grid, st);
       break;
+    case LQ_ROUND_SR_PHILOX:
+      launch_update<FB, LQ_ROUND_SR_PHILOX, LY>(p, vec, bcvec, grid, st);
+      break;
     default: launch_update<FB, LQ_ROUND_SR_COUNTER, LY>(p, vec, bcvec, grid, st); break;
   }
 }
@@ -1184,6 +1234,7 @@ static void dispatch_encode(const MxCodecParams& p, int rmode, bool vec, dim3 gr
     case LQ_ROUND_NEAREST_EVEN: launch_encode<FB, LQ_ROUND_NEAREST_EVEN, LY>(p, vec, grid, st); break;
     case LQ_ROUND_HALF_UP: launch_encode<FB, LQ_ROUND_HALF_UP, LY>(p, vec, grid, st); break;
     case LQ_ROUND_SR_UNIFORM: launch_encode<FB, LQ_ROUND_SR_UNIFORM, LY>(p, vec, grid, st); break;
+    case LQ_ROUND_SR_PHILOX: launch_encode<FB, LQ_ROUND_SR_PHILOX, LY>(p, vec, grid, st); break;
     default: launch_encode<FB, LQ_ROUND_SR_COUNTER, LY>(p, vec, grid, st); break;
   }
 }
@@ -1195,10 +1246,12 @@ static void dispatch_encode(const MxCodecParams& p, int rmode, bool vec, dim3 gr
 // build ran 42.2 against 41.4 us). The compact layouts move 2.5x fewer bytes and are bound by their arithmetic, so 4 rows
 // per lane share the per-lane setup (head scalars, B and C) over twice the rows: 41.1 -> 38.9 us
 // for MX4 at batch 64 (91 VGPRs, 5 waves per SIMD). The supplied-uniform mode keeps 2 rows per
-// lane everywhere: its 16 uniforms per row would take 155-161 VGPRs at 4 rows.
+// lane everywhere: its 16 uniforms per row would take 155-161 VGPRs at 4 rows. So does the Philox
+// mode, whose 4-row form kept the rows' arrays in scratch memory.
 template <int LY, int RMODE>
 struct RowsGeometry {
-  static constexpr bool wide = LY != LAYOUT_REF && RMODE != LQ_ROUND_SR_UNIFORM;
+  static constexpr bool wide =
+      LY != LAYOUT_REF && RMODE != LQ_ROUND_SR_UNIFORM && RMODE != LQ_ROUND_SR_PHILOX;
   static constexpr int R = wide ? 4 : 2;
   static constexpr int THREADS = wide ? 128 : 256;
   static_assert(R * THREADS == 512, "rows_per_workgroup assumes R * THREADS = 512");
@@ -1219,6 +1272,7 @@ static void launch_rows(const MxUpdateParams& p, int rmode, dim3 grid, hipStream
     case LQ_ROUND_NEAREST_EVEN: launch_rows_mode<FB, LQ_ROUND_NEAREST_EVEN, BPR_LOG2, LY>(p, grid, st); break;
     case LQ_ROUND_HALF_UP: launch_rows_mode<FB, LQ_ROUND_HALF_UP, BPR_LOG2, LY>(p, grid, st); break;
     case LQ_ROUND_SR_UNIFORM: launch_rows_mode<FB, LQ_ROUND_SR_UNIFORM, BPR_LOG2, LY>(p, grid, st); break;
+    case LQ_ROUND_SR_PHILOX: launch_rows_mode<FB, LQ_ROUND_SR_PHILOX, BPR_LOG2, LY>(p, grid, st); break;
     default: launch_rows_mode<FB, LQ_ROUND_SR_COUNTER, BPR_LOG2, LY>(p, grid, st); break;
   }
 }
@@ -1362,8 +1416,10 @@ static int mx_state_update(const lq_tensor* q_state, const lq_tensor* shared_exp
   p.softplus = dt_softplus != 0;
   p.a_row_const = A->stride[2] == 0;
   p.key = seed_key(seed);
+  p.pk0 = (uint32_t)seed;
+  p.pk1 = (uint32_t)(seed >> 32);
   p.rng_offset = rng_offset;
-  if (step != nullptr && round_mode == LQ_ROUND_SR_COUNTER) {
+  if (step != nullptr && (round_mode == LQ_ROUND_SR_COUNTER || round_mode == LQ_ROUND_SR_PHILOX)) {
     p.step_dev = (const int64_t*)step->data;
     p.step_stride = (uint64_t)(Bn * H * P * N);
   }
@@ -1501,6 +1557,8 @@ extern "C" int lq_mx_encode(const lq_tensor* state, const lq_tensor* q_state,
   p.bpr = (int)(N / 16);
   p.vbpr_log2 = log2_ceil(p.bpr);
   p.key = seed_key(seed);
+  p.pk0 = (uint32_t)seed;
+  p.pk1 = (uint32_t)(seed >> 32);
   p.rng_offset = rng_offset;
   const lq_tensor* spans[] = {q_state, shared_exp, micro_exp, state, uniform};
   for (const lq_tensor* t : spans) {

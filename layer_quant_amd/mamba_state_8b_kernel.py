@@ -15,8 +15,10 @@ torch initial encoder are replaced by HIP kernels for gfx950 behind the C ABI
 Stochastic rounding. The reference draws Triton's tl.rand per element at offset
 step*B*H*P*N + element index. This module keeps those offsets and, by default, draws from the
 library's counter-based generator (LQ_ROUND_SR_COUNTER, 16-bit uniforms from a hash of
-(seed, offset)). Passing `uniform=` (an fp32 tensor shaped like the state) rounds with those
-uniforms instead, for bit-exact comparison with any other implementation given the same tensor.
+(seed, offset)). `rng="philox"` draws the reference's own stream instead (LQ_ROUND_SR_PHILOX:
+tl.rand's Philox4x32-10 and the reference's u < frac test, bit for bit, at about 4x the counter
+mode's arithmetic). Passing `uniform=` (an fp32 tensor shaped like the state) rounds with those
+uniforms, for bit-exact comparison with any other implementation given the same tensor.
 `stochastic=False` selects the reference's deterministic floor(q + 0.5) writeback.
 """
 from __future__ import annotations
@@ -201,15 +203,19 @@ def mx_state_selective_update(cache: MambaStateKernelCache, x: torch.Tensor, dt:
                               D: torch.Tensor | None = None, z: torch.Tensor | None = None,
                               dt_bias: torch.Tensor | None = None, dt_softplus: bool = False,
                               stochastic: bool = True, seed: int = 1234, *,
-                              uniform: torch.Tensor | None = None) -> torch.Tensor:
+                              uniform: torch.Tensor | None = None,
+                              rng: str = "counter") -> torch.Tensor:
     """One fused decode step on the MX state, in place; returns y [B,H,P] in x's dtype
     (ms.py:601-721).
 
     h = dequant(state); dt (+ dt_bias, read with D's strides); softplus if dt_softplus;
     h' = h*exp(A*dt) + B*dt*x; y = sum_n h'*C (+ x*D) (* z); the state is re-encoded in its
-    format with stochastic rounding (counter generator or `uniform`) or, with
-    stochastic=False, floor(q + 0.5). cache.step advances by one.
+    format with stochastic rounding (the counter generator, rng="philox" for the reference's
+    tl.rand stream, or `uniform`) or, with stochastic=False, floor(q + 0.5). cache.step
+    advances by one.
     """
+    if rng not in ("counter", "philox"):
+        raise ValueError(f"rng must be 'counter' or 'philox', got {rng!r}")
     if cache.q_state.ndim != 4:
         raise ValueError(f"Expected q_state [B,H,P,N], got {tuple(cache.q_state.shape)}")
     batch, nheads, dim, dstate = cache.state_shape
@@ -224,9 +230,12 @@ def mx_state_selective_update(cache: MambaStateKernelCache, x: torch.Tensor, dt:
         mode = _abi.ROUND_HALF_UP
     elif uniform is not None:
         mode = _abi.ROUND_SR_UNIFORM
+    elif rng == "philox":
+        mode = _abi.ROUND_SR_PHILOX
     else:
         mode = _abi.ROUND_SR_COUNTER
-    on_device = cache.device_step is not None and mode == _abi.ROUND_SR_COUNTER
+    on_device = cache.device_step is not None and mode in (_abi.ROUND_SR_COUNTER,
+                                                           _abi.ROUND_SR_PHILOX)
     rng_offset = 0 if on_device else cache.step * batch * nheads * dim * dstate
     _abi.mx_state_update(cache.q_state, cache.shared_exp, cache.micro_exp, x, dt,
                          _dt_bias_as_read(dt_bias, D, nheads, dim), A, B, C, D, z, out,
@@ -242,10 +251,11 @@ def mx_state_selective_update(cache: MambaStateKernelCache, x: torch.Tensor, dt:
 
 def enable_device_step(cache: MambaStateKernelCache) -> MambaStateKernelCache:
     """Keep the cache's stochastic-rounding step counter on the device as well (int64 [1],
-    starting at cache.step): the counter-mode update then takes its offset step * B*H*P*N from
-    that tensor in the kernel and advances it with a tensor add, which a captured HIP graph
-    replays, so every replay rounds with fresh draws. cache.step still counts the host-side
-    calls. No counterpart in the reference (a host integer there, ms.py:659, 716)."""
+    starting at cache.step): the counter- and Philox-mode updates then take their offset
+    step * B*H*P*N from that tensor in the kernel and advance it with a tensor add, which a
+    captured HIP graph replays, so every replay rounds with fresh draws. cache.step still counts
+    the host-side calls. No counterpart in the reference (a host integer there, ms.py:659,
+    716)."""
     cache.device_step = torch.tensor([cache.step], dtype=torch.int64, device=cache.q_state.device)
     return cache
 
@@ -296,19 +306,24 @@ def selective_state_update(state: torch.Tensor, x: torch.Tensor, dt: torch.Tenso
 
 
 def patch_nemotron_h_mamba_decode_state_kernel(model, group_size: int = MX8_BLOCK_SIZE,
-                                               stochastic: bool = True, seed: int = 1234) -> None:
+                                               stochastic: bool = True, seed: int = 1234, *,
+                                               rng: str = "counter") -> None:
     """Rebind the remote module's selective_state_update (ms.py:732-767).
 
     States registered through register_mamba_state_kernel_caches (looked up by id) take the MX
-    update; any other state falls through to the original function. The rounding mode and seed
-    live on the module and may be changed by calling this again.
+    update; any other state falls through to the original function. The rounding mode, seed and
+    generator (rng="philox" for the reference's tl.rand stream) live on the module and may be
+    changed by calling this again.
     """
+    if rng not in ("counter", "philox"):
+        raise ValueError(f"rng must be 'counter' or 'philox', got {rng!r}")
     module = __import__(model.__class__.__module__, fromlist=["selective_state_update"])
     original = getattr(module, "_mx_state_kernel_original", module.selective_state_update)
     if original is None:  # the remote module found no mamba-ssm kernel: use the HIP update
         original = selective_state_update
     module._mx_state_kernel_stochastic = stochastic
     module._mx_state_kernel_seed = seed
+    module._mx_state_kernel_rng = rng
 
     def selective_state_update_mx(ssm_state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
                                   dt_softplus=False):
@@ -320,7 +335,8 @@ def patch_nemotron_h_mamba_decode_state_kernel(model, group_size: int = MX8_BLOC
         return mx_state_selective_update(
             mx_cache, x, dt, A, B, C, D=D, z=z, dt_bias=dt_bias, dt_softplus=dt_softplus,
             stochastic=getattr(module, "_mx_state_kernel_stochastic", True),
-            seed=getattr(module, "_mx_state_kernel_seed", 1234))
+            seed=getattr(module, "_mx_state_kernel_seed", 1234),
+            rng=getattr(module, "_mx_state_kernel_rng", "counter"))
 
     if not getattr(module, "_mx_state_kernel_patched", False):
         module.selective_state_update = selective_state_update_mx

@@ -14,8 +14,9 @@ Encode of a block with absmax a (ms.py:168-203, 512-534, 557-571):
 Rounding modes: nearest-even (torch.round, initial encode ms.py:568), half-up floor(qa + 0.5)
 (deterministic writeback ms.py:201, 482, 531), stochastic floor(qa) + (u < qa - floor(qa))
 (ms.py:196-199, 528-530) with u from a supplied tensor (ROUND_SR_UNIFORM, the reference's
-formula), and the counter mode ROUND_SR_COUNTER, which replaces the reference's Triton tl.rand
-draw by oracle.rng's 16-bit draws u16 used as a dither on a 2^-16 grid:
+formula) or from the reference's own generator (ROUND_SR_PHILOX: u = tl.rand(seed, rng_offset +
+index), oracle.philox), and the counter mode ROUND_SR_COUNTER, which replaces the reference's
+Triton tl.rand draw by oracle.rng's 16-bit draws u16 used as a dither on a 2^-16 grid:
     qs    = v / (base * 2^micro)                                  (signed, exact)
     t     = fp32(192 + u16 * 2^-16 + qs)                          (one rounding: the kernel's fma)
     level = floor(clamp(t, 192 - M, 193 + M - 2^-16)) - 192
@@ -60,7 +61,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from . import rng
+from . import philox, rng
 
 BLOCK = 16
 PAIR = 2
@@ -71,6 +72,7 @@ ROUND_NEAREST_EVEN = 0
 ROUND_HALF_UP = 1
 ROUND_SR_UNIFORM = 2
 ROUND_SR_COUNTER = 3
+ROUND_SR_PHILOX = 4
 
 # T(kk) for kk = -1..8, where the half spacing of fp32 around E is 2^(kk - 24).
 # T(kk) = largest j with log2(1 + j*2^-23) < 2^(kk-24)  (= floor(2^(kk-1) * ln 2) here).
@@ -155,7 +157,9 @@ def mx_encode(state, format_bits: int, round_mode: int = ROUND_NEAREST_EVEN,
         level = np.rint(qa)
     elif round_mode == ROUND_HALF_UP:
         level = np.floor(qa + np.float32(0.5))
-    elif round_mode == ROUND_SR_UNIFORM:
+    elif round_mode in (ROUND_SR_UNIFORM, ROUND_SR_PHILOX):
+        if round_mode == ROUND_SR_PHILOX:  # the reference's own draws: tl.rand per element
+            uniform = philox.state_uniforms(seed, rng_offset, v.shape)
         if uniform is None:
             raise ValueError("ROUND_SR_UNIFORM needs a uniform tensor")
         if isinstance(uniform, torch.Tensor):

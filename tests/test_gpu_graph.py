@@ -119,15 +119,18 @@ def test_decode_step_graph_replays_match_eager(gpu, mode):
     assert torch.isfinite(t["att"]).all()
 
 
+@pytest.mark.parametrize("rng", ["counter", "philox"])
 @pytest.mark.parametrize("path", ["rows", "general"])
-def test_device_step_graph_replays_draw_anew(gpu, diag, path):
-    """An MX4 counter-mode update through the module with its step counter on the device
-    (enable_device_step), captured together with the step's advance and replayed three times:
-    the states are bit-identical to three eager host-offset updates at offsets 0, T and 2T
-    (T = B*H*P*N), i.e. fresh draws on every replay, not three copies of one step's."""
+def test_device_step_graph_replays_draw_anew(gpu, diag, path, rng):
+    """An MX4 stochastic update (the counter generator, or the reference's Philox stream)
+    through the module with its step counter on the device (enable_device_step), captured
+    together with the step's advance and replayed three times: the states are bit-identical to
+    three eager host-offset updates at offsets 0, T and 2T (T = B*H*P*N), i.e. fresh draws on
+    every replay, not three copies of one step's."""
     from hybrid_quant import mamba_state_8b_kernel as ms
 
     diag.set("LQ_MX_REQUIRE_ROWS" if path == "rows" else "LQ_MX_FORCE_GENERIC")
+    mode = _abi.ROUND_SR_PHILOX if rng == "philox" else _abi.ROUND_SR_COUNTER
     t = _make_state(gpu, 99)
     bsz, nh, p_, n = t["st"][0].shape
     T = bsz * nh * p_ * n
@@ -138,8 +141,8 @@ def test_device_step_graph_replays_draw_anew(gpu, diag, path):
         snaps = []
         for off in offsets:
             _abi.mx_state_update(*st, t["x"], t["dt"], t["dt_bias"], t["A"], t["B"], t["C"],
-                                 t["D"], None, t["y"], 4, True, _abi.ROUND_SR_COUNTER,
-                                 seed=1234, rng_offset=off)
+                                 t["D"], None, t["y"], 4, True, mode, seed=1234,
+                                 rng_offset=off)
             torch.cuda.synchronize()
             snaps.append([a.clone() for a in st])
         return snaps
@@ -154,7 +157,8 @@ def test_device_step_graph_replays_draw_anew(gpu, diag, path):
     def step():
         # dt_bias as the module reads it (with D's strides, ms.py:137): the same tensor here
         return ms.mx_state_selective_update(cache, t["x"], t["dt"], t["A"], t["B"], t["C"],
-                                            D=t["D"], dt_bias=t["dt_bias"], dt_softplus=True)
+                                            D=t["D"], dt_bias=t["dt_bias"], dt_softplus=True,
+                                            rng=rng)
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())

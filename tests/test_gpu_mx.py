@@ -43,7 +43,7 @@ def _assert_mx_equal(gpu_t, ref):
 
 
 @pytest.mark.parametrize("fb", [8, 4])
-@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_encode_bit_exact(gpu, fb, mode, dtype):
     shape = (3, 8, 16, 128)
@@ -106,7 +106,7 @@ def _cpu(t):
 
 
 @pytest.mark.parametrize("fb", [8, 4])
-@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
 def test_update_dt_zero_writeback_bit_exact(gpu, path, fb, mode):
     shape = (2, 16, 8, 128)
     h0 = _state(shape, 30 + fb)
@@ -327,13 +327,15 @@ def test_full_size_b64_uniform_update_sampled_groups(gpu, fb):
 
 
 @pytest.mark.parametrize("fb", [8, 4])
-@pytest.mark.parametrize("mode", [_abi.ROUND_SR_UNIFORM, _abi.ROUND_SR_COUNTER])
+@pytest.mark.parametrize("mode", [_abi.ROUND_SR_UNIFORM, _abi.ROUND_SR_COUNTER,
+                                  _abi.ROUND_SR_PHILOX])
 def test_config3_batch1_full_layer_every_group(gpu, diag, fb, mode):
     """BASELINE configs 3 (MX8) and 4 (MX4) at batch 1 on the full Nemotron-H layer (128 heads x
     64 x 128, 8 groups): h0 ~ N(0, 0.5) encoded by the initial encoder, x ~ N(0, 1),
     dt = softplus(N(0, 1)) per head (passed with dt_softplus off), A = -exp(U(0, 2)), B, C ~ N(0, 1)
     per group, D ~ N(0, 1); the seeded supplied-uniform writeback (the configurations' own
-    rounding) or the counter generator; the model's layout, so the row kernel (required). The
+    rounding), the counter generator, or the reference's own tl.rand stream (Philox); the
+    model's layout, so the row kernel (required). The
     whole state -- every group -- against the oracle: y within 2e-3, the writeback to the
     assert_mx_writeback bar."""
     diag.set("LQ_MX_REQUIRE_ROWS")
@@ -370,12 +372,14 @@ def test_config3_batch1_full_layer_every_group(gpu, diag, fb, mode):
                         uniform=uni, seed=seed, rng_offset=off, what=f"state mx{fb} mode {mode}")
 
 
+@pytest.mark.parametrize("mode", [_abi.ROUND_SR_COUNTER, _abi.ROUND_SR_PHILOX])
 @pytest.mark.parametrize("fb", [4, 8])
-def test_counter_offsets_crossing_a_high_word_row_kernel(gpu, diag, fb):
-    """Counter offsets whose pair counters cross a 2^32 boundary of their high word inside one
-    launch (the row kernel switches the per-block hash of the high word where the low word
-    carries): the dt = 0 writeback is bit-exact against the oracle, through the host offset and
-    through a device step (lq_mx_state_update_device_step) giving the same offset."""
+def test_counter_offsets_crossing_a_high_word_row_kernel(gpu, diag, fb, mode):
+    """Offsets whose counters cross a 2^32 boundary of their high word inside one launch (the
+    row kernel switches the per-block hash of the high word where the low word carries; the
+    Philox counter's second word steps by one there): the dt = 0 writeback is bit-exact against
+    the oracle, through the host offset and through a device step
+    (lq_mx_state_update_device_step) giving the same offset."""
     diag.set("LQ_MX_REQUIRE_ROWS")
     shape = (2, 4, 16, 128)
     T = int(np.prod(shape))
@@ -391,11 +395,98 @@ def test_counter_offsets_crossing_a_high_word_row_kernel(gpu, diag, fb):
         out = torch.empty(2, 4, 16, device=gpu)
         if how == "host":
             _abi.mx_state_update(*st, t["x"], t["dt"], None, t["A"], t["B"], t["C"], None, None,
-                                 out, fb, False, 3, seed=77, rng_offset=base + 5 * T)
+                                 out, fb, False, mode, seed=77, rng_offset=base + 5 * T)
         else:
             _abi.mx_state_update(*st, t["x"], t["dt"], None, t["A"], t["B"], t["C"], None, None,
-                                 out, fb, False, 3, seed=77, rng_offset=base, step=step)
+                                 out, fb, False, mode, seed=77, rng_offset=base, step=step)
         torch.cuda.synchronize()
-        ref = omx.mx_encode(omx.mx_decode(q0, e0, m0), fb, omx.ROUND_SR_COUNTER, seed=77,
+        ref = omx.mx_encode(omx.mx_decode(q0, e0, m0), fb, mode, seed=77,
                             rng_offset=base + 5 * T)
         _assert_mx_equal(st, ref)
+
+
+@pytest.mark.parametrize("fb", [8, 4])
+@pytest.mark.parametrize("n", [64, 128, 96])
+def test_update_philox_mode_nonzero_dt(gpu, path, diag, fb, n):
+    """The reference's own rounding stream (LQ_ROUND_SR_PHILOX: u = tl.rand(seed, offset) per
+    element, the u < frac test) after a real update, on the row kernel's layout (d_state 64, 128;
+    96 on the general kernel) and with the general kernel forced: y within 2e-3, the state equal
+    to the oracle's except at encoder decision ties. The offsets run across 2^32 inside the
+    launch, so the counter's second word changes between rows."""
+    if n == 96:
+        diag.clear("LQ_MX_REQUIRE_ROWS")
+    bsz, nh, p_, ng = 2, 8, 40, 2
+    shape = (bsz, nh, p_, n)
+    h0 = _state(shape, 700 + fb + n)
+    q, e, m = omx.mx_encode(h0.numpy(), fb, 0)
+    t = _inputs(bsz, nh, p_, n, ng, 701, gpu, head_dt=True)
+    st = [torch.from_numpy(a).to(gpu) for a in (q, e, m)]
+    out = torch.empty(bsz, nh, p_, device=gpu)
+    off = (1 << 32) - int(np.prod(shape)) // 3
+    _abi.mx_state_update(*st, t["x"], t["dt"], t["dt_bias"], t["A"], t["B"], t["C"], t["D"], None,
+                         out, fb, True, _abi.ROUND_SR_PHILOX, seed=1234, rng_offset=off)
+    c = _cpu(t)
+    rq, re_, rm, ry, rh = omx.mx_update(q, e, m, c["x"], c["dt"], c["A"], c["B"], c["C"],
+                                        D=c["D"], dt_bias=c["dt_bias"], dt_softplus=True,
+                                        format_bits=fb, round_mode=omx.ROUND_SR_PHILOX,
+                                        seed=1234, rng_offset=off)
+    assert_close_rel(out.cpu(), ry, what="y")
+    mag = update_term_magnitudes(omx.mx_decode(q, e, m), c["x"], c["dt"], c["A"], c["B"],
+                                 c["C"], dt_bias=c["dt_bias"], dt_softplus=True)
+    assert_mx_writeback([a.cpu().numpy() for a in st], (rq, re_, rm), rh, mag, fb,
+                        omx.ROUND_SR_PHILOX, seed=1234, rng_offset=off, what="state")
+
+
+@pytest.mark.parametrize("fb", [8, 4])
+def test_philox_chain_module_api(gpu, fb):
+    """mx_state_selective_update(..., rng="philox"), 5 chained updates with dt = 0 (pure
+    re-encodes at the reference's offsets step*B*H*P*N, seed 1234 as the reference's default):
+    bit-exact with the oracle chain drawing tl.rand's stream."""
+    shape = (2, 8, 4, 128)
+    h0 = _state(shape, 720 + fb, torch.bfloat16)
+    cache = ms.allocate_state_kernel_cache(h0.to(gpu), format_bits=fb)
+    ref = omx.mx_encode(h0.float().numpy(), fb, 0)
+    t = _inputs(2, 8, 4, 128, 2, 721, gpu, dt_zero=True, head_dt=True)
+    c = _cpu(t)
+    for step in range(5):
+        ms.mx_state_selective_update(cache, t["x"], t["dt"], t["A"], t["B"], t["C"], D=t["D"],
+                                     rng="philox")
+        rq, re_, rm, _, _ = omx.mx_update(*ref, c["x"], c["dt"], c["A"], c["B"], c["C"],
+                                          D=c["D"], format_bits=fb,
+                                          round_mode=omx.ROUND_SR_PHILOX, seed=1234,
+                                          rng_offset=step * int(np.prod(shape)))
+        ref = (rq, re_, rm)
+        _assert_mx_equal((cache.q_state, cache.shared_exp, cache.micro_exp), ref)
+    assert cache.step == 5
+
+
+@pytest.mark.timeout(300)
+def test_full_size_b64_philox_dt_zero_sampled_slices(gpu, diag):
+    """Headline size (B=64, 128 heads x 64 x 128, MX4, the model's layout, the row kernel) with
+    the reference's stream at step 40 (offset 40*B*H*P*N, past 2^31, where the reference's int32
+    offsets no longer compile): the dt = 0 writeback of three (batch, head) slices bit-exact
+    against the oracle, each slice drawing offsets from (b*H + h)*P*N on."""
+    diag.set("LQ_MX_REQUIRE_ROWS")
+    bsz, nh, p_, n = 64, 128, 64, 128
+    shape = (bsz, nh, p_, n)
+    gen = torch.Generator(device=gpu).manual_seed(730)
+    h0 = torch.randn(shape, device=gpu, generator=gen) * 0.5
+    st = _mx_tensors(shape, gpu)
+    _abi.mx_encode(h0, *st, 4, 0)
+    del h0
+    st0 = [a.clone() for a in st]
+    x = torch.randn(bsz, nh, p_, device=gpu, generator=gen).to(torch.bfloat16)
+    dt = torch.zeros(bsz, nh, 1, device=gpu, dtype=torch.bfloat16).expand(bsz, nh, p_)
+    A = (-torch.rand(nh, device=gpu, generator=gen))[:, None, None].expand(nh, p_, n)
+    B = torch.randn(bsz, 8, n, device=gpu, generator=gen).to(torch.bfloat16)
+    C = torch.randn(bsz, 8, n, device=gpu, generator=gen).to(torch.bfloat16)
+    out = torch.empty(bsz, nh, p_, device=gpu, dtype=torch.bfloat16)
+    off = 40 * int(np.prod(shape))
+    _abi.mx_state_update(*st, x, dt, None, A, B, C, None, None, out, 4, False,
+                         _abi.ROUND_SR_PHILOX, seed=1234, rng_offset=off)
+    torch.cuda.synchronize()
+    for b, h in [(0, 0), (63, 127), (17, 90)]:
+        q, e, m = (a[b, h].cpu().numpy() for a in st0)
+        ref = omx.mx_encode(omx.mx_decode(q, e, m), 4, omx.ROUND_SR_PHILOX, seed=1234,
+                            rng_offset=off + (b * nh + h) * p_ * n)
+        _assert_mx_equal([a[b, h] for a in st], ref)

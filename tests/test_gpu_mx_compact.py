@@ -52,7 +52,7 @@ def path(request, diag):
 
 
 @pytest.mark.parametrize("fb", [4, 8])
-@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
 def test_encode_compact_is_oracle_compact(gpu, fb, mode):
     shape = (2, 4, 8, 128)
     h = _state(shape, 10 + fb)
@@ -86,7 +86,7 @@ def _inputs(bsz, nh, p_, n, ng, seed):
 
 
 @pytest.mark.parametrize("fb", [4, 8])
-@pytest.mark.parametrize("mode", [1, 2, 3])
+@pytest.mark.parametrize("mode", [1, 2, 3, 4])
 @pytest.mark.parametrize("n", [64, 128])
 def test_update_compact_equals_reference_layout(gpu, path, fb, mode, n):
     bsz, nh, p_, ng = 3, 16, 64, 4

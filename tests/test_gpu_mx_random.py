@@ -1,7 +1,7 @@
 """Seeded random sweep of MX state updates through the C ABI against the CPU oracle.
 
 Each case draws the format (MX8 / MX4), the rounding mode (nearest-even, half-up, supplied
-uniforms, counter), d_state (64, 128, 256 on the row kernel's layout; 96 on the general kernel),
+uniforms, counter; 24 further cases all take the reference's own Philox stream), d_state (64, 128, 256 on the row kernel's layout; 96 on the general kernel),
 head_dim (ragged against the row kernel's 64-row workgroups), batch, groups and heads per group,
 the dtypes of x and of the output, whether dt is constant along head_dim (the model's layout,
 taken by the row kernel) or not (general kernel), whether A varies along head_dim, whether
@@ -24,13 +24,13 @@ DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 Y_RTOL = {"f32": 2e-3, "f16": 3e-3, "bf16": 8e-3}  # the output's own rounding on top of 2e-3
 
 
-def _draw_cases(n, seed):
+def _draw_cases(n, seed, mode=None):
     rng = random.Random(seed)
     cases = []
     for i in range(n):
         c = dict(
             fb=rng.choice([8, 4]),
-            mode=rng.choice([0, 1, 2, 3]),
+            mode=rng.choice([0, 1, 2, 3]) if mode is None else mode,
             n=rng.choice([64, 128, 256, 128, 96]),
             p=rng.choice([16, 40, 64, 100]),
             bsz=rng.randint(1, 3),
@@ -52,6 +52,8 @@ def _draw_cases(n, seed):
 
 
 CASES = _draw_cases(96, 1202)
+# the reference's own stream (LQ_ROUND_SR_PHILOX), numbered after the cases above
+CASES += [(96 + i, c) for i, c in _draw_cases(24, 1303, mode=4)]
 
 
 @pytest.mark.parametrize("i,c", CASES, ids=[f"case{i}" for i, _ in CASES])

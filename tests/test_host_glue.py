@@ -144,6 +144,9 @@ def test_mx_argument_validation():
     with pytest.raises(ValueError, match="q_state"):
         ms.mx_state_selective_update(ms.MambaStateKernelCache(torch.zeros(2, 3), None, None),
                                      torch.zeros(2, 4, 8), torch.zeros(2, 4, 8), A, B, B)
+    with pytest.raises(ValueError, match="rng must be 'counter' or 'philox'"):
+        ms.mx_state_selective_update(cache, torch.zeros(2, 4, 8), torch.zeros(2, 4, 8), A, B, B,
+                                     rng="pcg")
 
 
 def test_dt_bias_is_read_with_D_strides():
