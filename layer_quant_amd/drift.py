@@ -1,14 +1,15 @@
 """Long-chain state drift of the MX4 / MX8 recurrent state against an unquantized state.
 
     python -m layer_quant_amd.drift [--batch 8] [--steps 2048] [--checkpoints 128,256,512,1024,2048]
-                                    [--rounding counter|uniform]
+                                    [--rounding counter|philox|uniform]
 
 Runs one Mamba2 layer of Nemotron-H-8B's shape (128 heads x 64 x 128, 8 groups) for --steps
 decode steps from one initial state h0 ~ N(0, 0.5), along four paths that see identical inputs:
 
     mx4   the MX4 state, fused update with stochastic writeback (counter generator, seed 1234,
-          the reference's step offsets; or, with --rounding uniform, a seeded uniform tensor
-          drawn per step and applied by the reference's floor(q) + (u < frac) rule)
+          the reference's step offsets; with --rounding philox the reference's own tl.rand
+          stream at those offsets; or, with --rounding uniform, a seeded uniform tensor drawn
+          per step and applied by the reference's floor(q) + (u < frac) rule)
                                                                  -- lq_mx_state_update
     mx8   the same with the MX8 format                             -- lq_mx_state_update
     bf16  a bf16 state, fp32 update, rounded back each step        -- lq_selective_state_update
@@ -49,10 +50,11 @@ def run(batch: int = 8, steps: int = 2048, checkpoints=(128, 256, 512, 1024, 204
     """The experiment; `record`, when given, receives CPU copies of h0, A, D and the inputs of
     the first `record_steps` steps (all steps by default) for replaying a short chain elsewhere,
     and with record_states = k the MX4 and MX8 states (q, shared_exp, micro_exp) after each of
-    the first k steps in record["states"]. `rounding` is "counter" (the library's generator) or
-    "uniform" (a uniform tensor per step from the seeded generator)."""
-    if rounding not in ("counter", "uniform"):
-        raise ValueError(f"rounding must be 'counter' or 'uniform', got {rounding!r}")
+    the first k steps in record["states"]. `rounding` is "counter" (the library's generator),
+    "philox" (the reference's tl.rand stream) or "uniform" (a uniform tensor per step from the
+    seeded generator)."""
+    if rounding not in ("counter", "philox", "uniform"):
+        raise ValueError(f"rounding must be 'counter', 'philox' or 'uniform', got {rounding!r}")
     dev = torch.device(device)
     gen = torch.Generator(device=dev).manual_seed(seed)
     shape = (batch, HEADS, DIM, DSTATE)
@@ -92,8 +94,9 @@ def run(batch: int = 8, steps: int = 2048, checkpoints=(128, 256, 512, 1024, 204
                                         uniform=None if uni is None else uni.cpu()))
         for bits in (4, 8):
             if uni is None:
+                mode = _abi.ROUND_SR_PHILOX if rounding == "philox" else _abi.ROUND_SR_COUNTER
                 _abi.mx_state_update(*mx[bits], x, dt, None, A, Bm, Cm, D, None,
-                                     outs[f"mx{bits}"], bits, False, _abi.ROUND_SR_COUNTER,
+                                     outs[f"mx{bits}"], bits, False, mode,
                                      seed=1234, rng_offset=(step - 1) * total)
             else:
                 _abi.mx_state_update(*mx[bits], x, dt, None, A, Bm, Cm, D, None,
@@ -121,8 +124,11 @@ def run(batch: int = 8, steps: int = 2048, checkpoints=(128, 256, 512, 1024, 204
         "steps": steps,
         "shape": list(shape),
         "groups": GROUPS,
-        "rounding": ("stochastic writeback, counter generator, seed 1234" if rounding == "counter"
-                     else "stochastic writeback, seeded uniform tensor per step (floor(q) + (u < frac))"),
+        "rounding": {
+            "counter": "stochastic writeback, counter generator, seed 1234",
+            "philox": "stochastic writeback, the reference's tl.rand (Philox4x32-10) stream, seed 1234",
+            "uniform": "stochastic writeback, seeded uniform tensor per step (floor(q) + (u < frac))",
+        }[rounding],
         "inputs": "fresh per step: x ~ N(0,1) bf16, dt = softplus(N(0,1)) per (batch, head), "
                   "B, C ~ N(0,1) bf16; fixed A = -exp(U(0,2)), D ~ N(0,1) per head; "
                   f"h0 ~ N(0, 0.5); generator seed {seed}",
@@ -137,7 +143,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--checkpoints", default="128,256,512,1024,2048")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--rounding", choices=["counter", "uniform"], default="counter")
+    ap.add_argument("--rounding", choices=["counter", "philox", "uniform"], default="counter")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("the drift experiment needs a GPU", file=sys.stderr)

@@ -174,11 +174,12 @@ def test_full_size_b64_model_layout(gpu, path):
                          what=f"y batch {b}")
 
 
-@pytest.mark.parametrize("rounding", ["counter", "uniform"])
+@pytest.mark.parametrize("rounding", ["counter", "philox", "uniform"])
 def test_drift_tool_replays_on_the_oracle(gpu, rounding):
     """layer_quant_amd.drift on a short chain (batch 1, 6 steps): the reported drift of the MX4
     state, the bf16 state and y agrees with the same chain replayed through the CPU oracle, with
-    the counter generator and with the supplied per-step uniform tensors."""
+    the counter generator, the reference's Philox stream and the supplied per-step uniform
+    tensors."""
     import numpy as np
 
     from layer_quant_amd import drift
@@ -192,8 +193,9 @@ def test_drift_tool_replays_on_the_oracle(gpu, rounding):
     total = rec["h0"].numel()
     got = {}
     for i, s in enumerate(rec["steps"], start=1):
-        if rounding == "counter":
-            mode = dict(round_mode=omx.ROUND_SR_COUNTER, seed=1234, rng_offset=(i - 1) * total)
+        if rounding in ("counter", "philox"):
+            mode = dict(round_mode=omx.ROUND_SR_COUNTER if rounding == "counter"
+                        else omx.ROUND_SR_PHILOX, seed=1234, rng_offset=(i - 1) * total)
         else:
             mode = dict(round_mode=omx.ROUND_SR_UNIFORM, uniform=s["uniform"].numpy())
         q, e, m, y4, _ = omx.mx_update(q, e, m, s["x"], s["dt"], rec["A"], s["B"], s["C"],
@@ -245,8 +247,8 @@ def _replay_slices(rec, bits, steps, slices):
 def test_config4_chain_2048_steps(gpu):
     """one Nemotron-H Mamba2 layer at batch 8 run for 2048 decode steps in
     MX4 and MX8 next to a bf16 and an fp32 state (layer_quant_amd.drift), with the
-    configuration's own rounding (a seeded uniform tensor per step) and with the counter
-    generator. Checks: every figure finite; MX8 drift below MX4's at every checkpoint; no growth
+    configuration's own rounding (a seeded uniform tensor per step), with the counter generator
+    and with the reference's own tl.rand stream (Philox). Checks: every figure finite; MX8 drift below MX4's at every checkpoint; no growth
     of the MX4 state drift from step 128 to 2048 beyond +-15%; the bf16 state within 1% of
     fp32; and the first 16 steps of the uniform run replayed through the oracle from the GPU's
     state before each step on four (batch, group) slices, equal except at encoder decision
@@ -257,7 +259,7 @@ def test_config4_chain_2048_steps(gpu):
     from layer_quant_amd import drift
 
     marks = (128, 256, 512, 1024, 2048)
-    for rounding in ("uniform", "counter"):
+    for rounding in ("uniform", "counter", "philox"):
         rec = {}
         res = drift.run(batch=8, steps=2048, checkpoints=marks, rounding=rounding,
                         record=rec if rounding == "uniform" else None,
