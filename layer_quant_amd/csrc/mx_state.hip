@@ -169,11 +169,13 @@ __device__ __forceinline__ float philox_uniform(uint32_t k0, uint32_t k1, uint64
   uint32_t c0 = (uint32_t)c, c1 = (uint32_t)(c >> 32), c2 = 0u, c3 = 0u;
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
-    const uint32_t a0 = c0, a2 = c2;
-    c0 = __umulhi(RB, a2) ^ c1 ^ k0;
-    c2 = __umulhi(RA, a0) ^ c3 ^ k1;
-    c1 = RB * a2;
-    c3 = RA * a0;
+    // one 32 x 32 -> 64-bit product per multiplier (v_mad_u64_u32 gives both halves at the cost
+    // of one v_mul_hi_u32) and one three-way xor (v_bitop3_b32, full rate) per word
+    const uint64_t pa = (uint64_t)RA * c0, pb = (uint64_t)RB * c2;
+    c0 = __builtin_amdgcn_bitop3_b32((uint32_t)(pb >> 32), c1, k0, 0x96);
+    c2 = __builtin_amdgcn_bitop3_b32((uint32_t)(pa >> 32), c3, k1, 0x96);
+    c1 = (uint32_t)pb;
+    c3 = (uint32_t)pa;
     k0 += KA;
     k1 += KB;
   }

@@ -16,8 +16,8 @@ Stochastic rounding. The reference draws Triton's tl.rand per element at offset
 step*B*H*P*N + element index. This module keeps those offsets and, by default, draws from the
 library's counter-based generator (LQ_ROUND_SR_COUNTER, 16-bit uniforms from a hash of
 (seed, offset)). `rng="philox"` draws the reference's own stream instead (LQ_ROUND_SR_PHILOX:
-tl.rand's Philox4x32-10 and the reference's u < frac test, bit for bit, at about 4x the counter
-mode's arithmetic). Passing `uniform=` (an fp32 tensor shaped like the state) rounds with those
+tl.rand's Philox4x32-10 and the reference's u < frac test, bit for bit, at about 2.7x the counter
+mode's time). Passing `uniform=` (an fp32 tensor shaped like the state) rounds with those
 uniforms, for bit-exact comparison with any other implementation given the same tensor.
 `stochastic=False` selects the reference's deterministic floor(q + 0.5) writeback.
 """
@@ -52,9 +52,9 @@ class MambaStateKernelCache:
     format_bits: int = 8
     step: int = 0
     layout: str = "reference"
-    # optional step counter on the device (int64 [1], see enable_device_step): the counter
-    # rounding then reads it in the kernel and advances it with a tensor add, so a decode step
-    # captured in a graph draws anew on every replay
+    # optional step counter on the device (int64 [1], see enable_device_step): the counter and
+    # Philox roundings then read it in the kernel and advance it with a tensor add, so a decode
+    # step captured in a graph draws anew on every replay
     device_step: torch.Tensor | None = None
 
     @property
