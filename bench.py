@@ -283,8 +283,10 @@ def build_workload(torch, args, dev):
     return attn, mamba, sizes
 
 
-def run_step(torch, args, attn, mamba, ev=None):
+def run_step(torch, args, attn, mamba, ev=None, round_mode=None):
     from layer_quant_amd import _abi
+
+    mode = _abi.ROUND_SR_COUNTER if round_mode is None else round_mode
 
     B, S, g = args.batch, args.ctx, args.group
     total_state = B * 128 * 64 * 128
@@ -310,8 +312,7 @@ def run_step(torch, args, attn, mamba, ev=None):
             off = M["step"] * total_state
             _abi.mx_state_update(
                 *M["st"], M["x"], M["dt"], M["dt_bias"], M["A"], M["B"], M["C"], M["D"], None,
-                M["out"], args.state_bits, True, _abi.ROUND_SR_COUNTER, seed=1234,
-                rng_offset=off)
+                M["out"], args.state_bits, True, mode, seed=1234, rng_offset=off)
             M["step"] += 1
 
     if mamba:
@@ -788,6 +789,29 @@ def layout_pair(torch, args, dev, mamba, ref_us):
             "compact_over_reference_time": round(us / ref_us, 4)}
 
 
+def rng_pair(torch, args, mamba, ref_us):
+    """The step's MX updates on the line's own states with the reference's rounding stream
+    (LQ_ROUND_SR_PHILOX: Triton's tl.rand per element, generated in the kernel), timed as the
+    line's counter-mode updates (one event pair around each step's run of back-to-back
+    updates)."""
+    from layer_quant_amd import _abi
+
+    for _ in range(3):
+        run_step(torch, args, [], mamba, round_mode=_abi.ROUND_SR_PHILOX)
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    for _ in range(args.steps):
+        run_step(torch, args, [], mamba, ev, round_mode=_abi.ROUND_SR_PHILOX)
+    torch.cuda.synchronize()
+    us = ev.mean_us("mx_update")
+    return {"what": (f"the step's {len(mamba)} MX{args.state_bits} updates with the reference's "
+                     "own stochastic-rounding stream (Triton tl.rand, Philox4x32-10, per element "
+                     "in the kernel; bit-exact with the reference's draws) instead of the "
+                     "library's counter generator"),
+            "counter_us": round(ref_us, 2), "philox_us": round(us, 2),
+            "philox_over_counter_time": round(us / ref_us, 3)}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -882,6 +906,11 @@ def main():
         log("compact-layout MX updates")
         pair = layout_pair(torch, args, dev, mamba, kernels["mx_update"]["us"])
         log(f"compact layout: {pair['compact_us']} us/call against {pair['reference_us']} us")
+    rng = None
+    if mamba and args.state_layout == "reference":
+        log("MX updates with the reference's Philox stream")
+        rng = rng_pair(torch, args, mamba, kernels["mx_update"]["us"])
+        log(f"Philox rounding: {rng['philox_us']} us/call against {rng['counter_us']} us")
     cfg1_gpu = config1_gpu(torch, dev)
     log("the reference's published shape")
     ref_shape = reference_shape(torch, dev)
@@ -932,6 +961,7 @@ def main():
         "cpu_baseline": cpu,
         "config1_cpu_vs_gpu": cfg1,
         "layout_pair": pair,
+        "rng_pair": rng,
         "reference_shape": ref_shape,
     }
     print(json.dumps(line), flush=True)
