@@ -62,10 +62,11 @@ def parse_args():
                     help="after the timed steps, time the same MX updates on compact-layout "
                          "states (layout_pair in the line; reference-layout runs only)")
     ap.add_argument("--sweep", nargs="?", const="all", default=None,
-                    choices=["all", "attention", "state", "prefill"],
+                    choices=["all", "attention", "state", "prefill", "pack"],
                     help="instead of the decode step, time each kernel alone over the BASELINE "
                          "configurations (attention: batch 1/8/64 x ctx 1K/4K/16K; MX8, MX4 and "
-                         "bf16 state updates: batch 1/8/64; INT4 prefill: L 1K/4K/16K), each call "
+                         "bf16 state updates: batch 1/8/64; INT4 prefill: L 1K/4K/16K; the K+V "
+                         "pack of a prompt, L 1K/4K/16K, and of one decode token), each call "
                          "after a 512 MB scratch read so that nothing is cache-resident; prints "
                          "one JSON line. An argument restricts it to one kernel family")
     ap.add_argument("--batches", default=None,
@@ -73,7 +74,7 @@ def parse_args():
     ap.add_argument("--ctxs", default=None,
                     help="--sweep attention: comma-separated contexts to keep (default: all)")
     ap.add_argument("--lengths", default=None,
-                    help="--sweep prefill: comma-separated prompt lengths (default 1024,4096,16384)")
+                    help="--sweep prefill / pack: comma-separated prompt lengths (default 1024,4096,16384)")
     ap.add_argument("--reps", type=int, default=20,
                     help="--sweep: timed calls per configuration (median reported)")
     ap.add_argument("--cpu-pairs", choices=["on", "off"], default="on",
@@ -330,8 +331,8 @@ def sweep(torch, dev, args):
     from concurrent.futures import ThreadPoolExecutor
 
     from layer_quant_amd import _abi
-    from layer_quant_amd.traffic import (attention_bytes, mx_update_bytes, prefill_flops,
-                                         ssm_update_bytes)
+    from layer_quant_amd.traffic import (attention_bytes, mx_update_bytes, pack_bytes,
+                                         prefill_flops, ssm_update_bytes)
     from oracle import int4_kv as oik
     from oracle import mx_state as omx
 
@@ -481,6 +482,24 @@ def sweep(torch, dev, args):
                      "oracle.mx_state.bf16_state_update (torch fp32, intra-op threads), same "
                      "state and inputs")
         rows.append(r)
+    # the K+V pack of one attention layer (lq_int4_pack_kv_pair, one launch): a prompt's tokens
+    # at batch 1 (the prefill's pack, int4_8b_attention.py:477-515 with q_len = L) and one decode
+    # token at batch 64 (the standalone pack; the decode step packs inside the attention)
+    for B, T in ([(1, L) for L in lengths] + [(64, 1)] if which in ("all", "pack") else ()):
+        if not want(B):
+            continue
+        kx = torch.randn(B, hkv, T, d, device=dev, generator=gen).to(torch.bfloat16)
+        vx = torch.randn(B, hkv, T, d, device=dev, generator=gen).to(torch.bfloat16)
+        cap = T if T > 1 else 16384
+        kp = torch.empty(B, hkv, cap, d // 2, dtype=torch.uint8, device=dev)
+        vp = torch.empty_like(kp)
+        ks = torch.empty(B, hkv, cap, d // g, device=dev)
+        vs = torch.empty_like(ks)
+        pos = torch.arange(T, device=dev) + (cap - T)
+        med, mean = timed(lambda: _abi.int4_pack_kv_pair(kx, vx, kp, vp, ks, vs, pos, g))
+        rows.append(row("int4_pack_kv_pair", 2 * pack_bytes(B, hkv, T, d, g), med, mean,
+                        batch=B, tokens=T, group=g))
+        del kx, vx, kp, vp, ks, vs
     for L in (lengths if which in ("all", "prefill") else ()):
         # causal prefill over the packed cache of one attention layer, batch 1 (MFMA-bound); no
         # CPU pair: the float64 oracle's L x L scores at L = 16384 need 69 GB

@@ -105,6 +105,90 @@ def test_pack_edge_values(gpu):
     assert ref_s[0, 0, 0, 0].item() == torch.tensor(1e-8).item()
 
 
+@pytest.mark.parametrize("g,d", [(8, 128), (16, 128), (32, 128), (64, 128), (128, 128),
+                                 (256, 256), (32, 64)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_pack_prompt_sized_bit_exact(gpu, g, d, dtype):
+    """A prompt's worth of tokens per (batch, head) (96, shuffled positions, outlier channels,
+    a token of zeros): the group-per-lane kernel (g 16 / 32 / 64) and the 8-values-per-lane row
+    kernel (other g), both bit-exact against the oracle, K and V in one pair call."""
+    b, h, t = 2, 3, 96
+    k = _activations((b, h, t, d), 300 + g + d, dtype)
+    v = _activations((b, h, t, d), 400 + g + d, dtype)
+    k[1, 2, 5] = 0
+    pos = torch.randperm(t, generator=torch.Generator().manual_seed(g))
+    cap = t + 4
+    kp = torch.full((b, h, cap, d // 2), 0xAB, dtype=torch.uint8, device=gpu)
+    vp = torch.full_like(kp, 0xCD)
+    ks = torch.full((b, h, cap, d // g), -1.0, device=gpu)
+    vs = torch.full_like(ks, -2.0)
+    _abi.int4_pack_kv_pair(k.to(gpu), v.to(gpu), kp, vp, ks, vs, pos.to(gpu), g)
+    ref_kp = torch.full((b, h, cap, d // 2), 0xAB, dtype=torch.uint8)
+    ref_vp = torch.full_like(ref_kp, 0xCD)
+    ref_ks = torch.full((b, h, cap, d // g), -1.0)
+    ref_vs = torch.full_like(ref_ks, -2.0)
+    oik.pack_into(ref_kp, ref_ks, k, pos, g)
+    oik.pack_into(ref_vp, ref_vs, v, pos, g)
+    assert torch.equal(kp.cpu(), ref_kp) and torch.equal(vp.cpu(), ref_vp)
+    assert torch.equal(ks.cpu(), ref_ks) and torch.equal(vs.cpu(), ref_vs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_pack_near_ties_bit_exact(gpu, dtype):
+    """Values whose quotient by the group scale lies within 2^-24 .. 2^-12 of a half-integer
+    (both sides), under 256 different non-power-of-two scales: the row kernel's product with the
+    reciprocal, and its IEEE-division fallback near half-integers, give the oracle's levels."""
+    gen = torch.Generator().manual_seed(77)
+    rows, d, g = 256, 128, 32
+    s = (torch.rand(rows, d // g, 1, generator=gen) * 3 + 0.1)  # target scales
+    k = torch.randint(-7, 7, (rows, d // g, g), generator=gen).float()
+    dl = 2.0 ** -torch.randint(12, 25, (rows, d // g, g), generator=gen).float()
+    sign = torch.where(torch.rand(rows, d // g, g, generator=gen) < 0.5, -1.0, 1.0)
+    x = (k + 0.5 + sign * dl) * s
+    x[:, :, 0] = 7.0 * s[:, :, 0]  # the group's absmax: scale = RN(7 s / 7)
+    x = x.reshape(1, 1, rows, d).to(dtype)
+    pos = torch.arange(rows)
+    packed = torch.zeros(1, 1, rows, d // 2, dtype=torch.uint8, device=gpu)
+    scale = torch.zeros(1, 1, rows, d // g, device=gpu)
+    _abi.int4_pack_kv(x.to(gpu), packed, scale, pos.to(gpu), g)
+    ref_p = torch.zeros(1, 1, rows, d // 2, dtype=torch.uint8)
+    ref_s = torch.zeros(1, 1, rows, d // g)
+    oik.pack_into(ref_p, ref_s, x, pos, g)
+    assert torch.equal(scale.cpu(), ref_s)
+    assert torch.equal(packed.cpu(), ref_p)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_pack_unaligned_rows_take_the_lane_kernel(gpu, dtype):
+    """Token rows that are not 16-byte aligned (a view starting one element into wider rows)
+    take the one-lane-per-byte kernel; both layouts give the oracle's bytes, and a prompt-sized
+    pair call (batch 1, 8 KV heads, 4096 tokens, aligned) takes the row kernel."""
+    d, g = 128, 32
+    wide = _activations((2, 4, 6, d + 1), 90, dtype)
+    x = wide[..., 1:]  # data pointer 2 bytes past a 16-byte boundary
+    pos = torch.tensor([5, 1, 0, 3, 2, 4])
+    packed = torch.zeros(2, 4, 6, d // 2, dtype=torch.uint8, device=gpu)
+    scale = torch.zeros(2, 4, 6, d // g, device=gpu)
+    _abi.int4_pack_kv(wide.to(gpu)[..., 1:], packed, scale, pos.to(gpu), g)
+    ref_p = torch.zeros(2, 4, 6, d // 2, dtype=torch.uint8)
+    ref_s = torch.zeros(2, 4, 6, d // g)
+    oik.pack_into(ref_p, ref_s, x, pos, g)
+    assert torch.equal(packed.cpu(), ref_p) and torch.equal(scale.cpu(), ref_s)
+    t = 4096
+    k = _activations((1, 8, t, d), 91, dtype)
+    v = _activations((1, 8, t, d), 92, dtype)
+    pos = torch.arange(t)
+    kp = torch.zeros(1, 8, t, d // 2, dtype=torch.uint8, device=gpu)
+    vp = torch.zeros_like(kp)
+    ks = torch.zeros(1, 8, t, d // g, device=gpu)
+    vs = torch.zeros_like(ks)
+    _abi.int4_pack_kv_pair(k.to(gpu), v.to(gpu), kp, vp, ks, vs, pos.to(gpu), g)
+    ref = oik.allocate_cache(1, 8, t, d, g)
+    oik.pack_kv_into_cache(ref, k, v, pos, g)
+    assert torch.equal(kp.cpu(), ref["k_packed"]) and torch.equal(vp.cpu(), ref["v_packed"])
+    assert torch.equal(ks.cpu(), ref["k_scale"]) and torch.equal(vs.cpu(), ref["v_scale"])
+
+
 def _packed_cache(b, hkv, s, d, g, seed, cap=None):
     cap = cap or s
     cache = oik.allocate_cache(b, hkv, cap, d, g)
