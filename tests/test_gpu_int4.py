@@ -111,10 +111,11 @@ def test_pack_edge_values(gpu):
 def test_pack_prompt_sized_bit_exact(gpu, g, d, dtype):
     """A prompt's worth of tokens per (batch, head) (96, shuffled positions, outlier channels,
     a token of zeros): the group-per-lane kernel (g 16 / 32 / 64) and the 8-values-per-lane row
-    kernel (other g), both bit-exact against the oracle, K and V in one pair call."""
+    kernel (other g), both bit-exact against the oracle, K and V in one pair call; V given as the
+    model's transposed view ([B, L, Hkv, D] -> [B, Hkv, L, D])."""
     b, h, t = 2, 3, 96
     k = _activations((b, h, t, d), 300 + g + d, dtype)
-    v = _activations((b, h, t, d), 400 + g + d, dtype)
+    v = _activations((b, t, h, d), 400 + g + d, dtype).transpose(1, 2)
     k[1, 2, 5] = 0
     pos = torch.randperm(t, generator=torch.Generator().manual_seed(g))
     cap = t + 4
