@@ -27,7 +27,8 @@
 //     2^e multiplies the score inside the softmax's exp2 argument.
 //   O^T[dim][query]: A = V^T rows (exact integers) of the dims of group m, B = P'_m with
 //     P'_m[key][query] = p[key][query] * vscale[key][m] / vmax_m split into fp16 hi + lo (two
-//     MFMAs, about 22 significant bits), vmax_m the power of two at or above the largest V scale of group m over the
+//     MFMAs, about 22 significant bits; hi the fp16 product of p and the scale rounded to fp16,
+//     lo the fp32 remainder rounded to fp16), vmax_m the power of two at or above the largest V scale of group m over the
 //     workgroup's keys (one pre-pass over the scales), so P'_m <= 2^8 never overflows fp16; the
 //     output tiles of group m are multiplied by vmax_m at the end.
 // Softmax runs in the exp2 domain with a lazily moved running max (rescale only when a score
@@ -100,6 +101,7 @@ struct alignas(16) PrefillLds {
   uint16_t v[2][PD][VROW];
   float ks[2][G][KT];
   float vs[2][G][KT];
+  uint16_t vp[2][G][KT];  // vs as fp16, in the P V B-operand order (vpair_slot)
   float vred[NW][G];
 };
 
@@ -135,6 +137,11 @@ __device__ __forceinline__ void load_tile(const uint8_t* kb, const uint8_t* vb, 
   r.sc = (si < G * KT && sk < L) ? sb[(int64_t)sk * G + (si / KT)] : 0.0f;
 }
 
+// key k of a tile -> its half-word in the fp16 V-scale row: lane group j's B-operand key pairs
+// (16t + 4j + r, r + 1), t = u >> 1, r = 2 (u & 1), are dword 4j + u, so a lane reads its four
+// pairs with one 16-byte load
+__device__ __forceinline__ int vpair_slot(int k) { return 8 * ((k >> 2) & 3) + 4 * (k >> 4) + (k & 3); }
+
 // key k of a tile -> its column in the V^T tile: lane group j's keys 4j..4j+3 and 16+4j..16+4j+3
 // (its K slots 0..7 of the P V product) sit at columns 8j .. 8j+7
 __device__ __forceinline__ int vcol(int k) { return 8 * ((k >> 2) & 3) + 4 * (k >> 4) + (k & 3); }
@@ -169,7 +176,9 @@ __device__ __forceinline__ void stage_tile(PrefillLds<G>& s, int nb, const RawTi
     if (tid < 128) {
       s.ks[nb][m][key] = r.sc * scale_sm;
     } else {
-      s.vs[nb][m][key] = r.sc * vinv[m];
+      const float v = r.sc * vinv[m];
+      s.vs[nb][m][key] = v;
+      s.vp[nb][m][vpair_slot(key)] = __builtin_bit_cast(uint16_t, (_Float16)v);
     }
   }
 }
@@ -397,13 +406,25 @@ void prefill_mfma_kernel(PrefillParams p) {
     // section issues first, the other's QK and softmax work filling in behind it (L = 16384:
     // 4.47 against 4.89 ms; the same over the QK products gains nothing)
     __builtin_amdgcn_s_setprio(1);
+    // B operand slots 2u, 2u+1 = keys (t, r) = (u >> 1, 2(u & 1)) and (u >> 1, 2(u & 1) + 1)
+    uint32_t p16[2][4];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        p16[qt][u] = pack_f16(pr[qt][u >> 1][2 * (u & 1)], pr[qt][u >> 1][2 * (u & 1) + 1]);
+      }
+    }
 #pragma unroll
     for (int m = 0; m < G; ++m) {
       f32x4_t vs4[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t) vs4[t] = *(const f32x4_t*)&lds.vs[nb][m][16 * t + 4 * j4];
-      // B operand slots 2u, 2u+1 = keys (t, r) = (u >> 1, 2(u & 1)) and (u >> 1, 2(u & 1) + 1);
-      // P'_m as fp16 hi + lo (about 22 significant bits)
+      const u32x4_t vs16 = *(const u32x4_t*)&lds.vp[nb][m][8 * j4];
+      // P'_m = p * vs as fp16 hi + lo (about 22 significant bits): hi = RN(RN16(p) * RN16(vs))
+      // by one packed fp16 multiply per pair, within 2^-10 of p * vs; lo = RN16(p * vs - hi)
+      // with p * vs exact inside the fused multiply-add (four instructions per pair; rounding
+      // p * vs itself to fp16 took two fp32 multiplies and a conversion for hi)
       u32x4_t bhi[2], blo[2];
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
@@ -411,12 +432,13 @@ void prefill_mfma_kernel(PrefillParams p) {
         for (int u = 0; u < 4; ++u) {
           const int t = u >> 1;
           const int r = 2 * (u & 1);
-          const float a0 = pr[qt][t][r] * vs4[t][r];
-          const float a1 = pr[qt][t][r + 1] * vs4[t][r + 1];
-          const uint32_t h = pack_f16(a0, a1);
-          const f16x2_t hh = __builtin_bit_cast(f16x2_t, h);
-          bhi[qt][u] = h;
-          blo[qt][u] = pack_f16(a0 - (float)hh[0], a1 - (float)hh[1]);
+          // (the element is copied out first: __builtin_bit_cast of an ext_vector element reads
+          // element 0 whatever the index with this compiler)
+          const uint32_t vw = vs16[u];
+          const f16x2_t hh = __builtin_bit_cast(f16x2_t, p16[qt][u]) * __builtin_bit_cast(f16x2_t, vw);
+          bhi[qt][u] = __builtin_bit_cast(uint32_t, hh);
+          blo[qt][u] = pack_f16(__builtin_fmaf(pr[qt][t][r], vs4[t][r], -(float)hh[0]),
+                                __builtin_fmaf(pr[qt][t][r + 1], vs4[t][r + 1], -(float)hh[1]));
         }
       }
 #pragma unroll
