@@ -4,7 +4,8 @@ dtypes and optional inputs (the fixed cases of the other test files pin the name
 
 * pack (hybrid_quant/int4_8b_attention.py:32-111, 477-515): bytes and scales bit-exact, single
   and K+V-pair entry points, head_dim 64/96/128/256, every even group dividing it, bf16/fp16/fp32
-  inputs, random distinct positions in a larger cache.
+  inputs, random distinct positions in a larger cache; prompt-sized packs (16-600 tokens per
+  (batch, head), g 8-256, V as a transposed view in some) for the group-per-lane and row kernels.
 * prefill (:114-251, 594-625): within 2e-3 of the float64 oracle (8e-3 for bf16 outputs), MFMA
   path (bf16 queries) and generic path (fp32), prompts of 1-300 tokens, group 32/64/128, 1-8
   query heads per KV head.
@@ -73,6 +74,57 @@ def test_pack_random(gpu, i, b, h, t, d, g, dt, pair):
         ref_p = torch.full((b, h, cap, d // 2), fill, dtype=torch.uint8)
         ref_s = torch.full((b, h, cap, d // g), sfill)
         oik.pack_into(ref_p, ref_s, x, pos, g)
+        assert torch.equal(p_dev.cpu(), ref_p)
+        assert torch.equal(s_dev.cpu(), ref_s)
+
+
+def _prompt_pack_cases(n, seed):
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        d = rng.choice([64, 128, 256])
+        g = rng.choice([gg for gg in (8, 16, 24, 32, 48, 64, 128, 256) if d % gg == 0])
+        b, h = rng.randint(1, 2), rng.choice([1, 2, 8])
+        out.append((i, b, h, rng.randint(max(16, 2048 // d), 600 if b * h <= 2 else 160), d, g,
+                    rng.choice(["bf16", "f16", "f32"]), rng.random() < 0.6, rng.random() < 0.5,
+                    rng.random() < 0.5))
+    return out
+
+
+PROMPT_PACK_CASES = _prompt_pack_cases(24, 2026)
+
+
+@pytest.mark.parametrize("i,b,h,t,d,g,dt,pair,vt,shuffled", PROMPT_PACK_CASES,
+                         ids=[f"case{c[0]}" for c in PROMPT_PACK_CASES])
+def test_pack_random_prompt(gpu, i, b, h, t, d, g, dt, pair, vt, shuffled):
+    """Prompt-sized packs (many tokens per (batch, head), so the group-per-lane and the row
+    kernels take them where their layouts allow): bit-exact against the oracle, with V as the
+    model's transposed view in some cases and the positions shuffled or offset."""
+    print(f"[prompt pack case {i}] b={b} h={h} t={t} d={d} g={g} {dt} pair={pair} vt={vt}",
+          flush=True)
+    gen = torch.Generator().manual_seed(700 + i)
+    cap = t + int(torch.randint(0, 20, (1,), generator=gen))
+    pos = torch.randperm(cap, generator=gen)[:t] if shuffled else torch.arange(t) + (cap - t)
+    k = _activations((b, h, t, d), gen).to(DTYPES[dt])
+    if vt:
+        v = _activations((b, t, h, d), gen).to(DTYPES[dt]).transpose(1, 2)
+    else:
+        v = _activations((b, h, t, d), gen).to(DTYPES[dt])
+    k[0, 0, t // 2] = 0
+    kp = torch.full((b, h, cap, d // 2), 0x3C, dtype=torch.uint8, device=gpu)
+    vp = torch.full_like(kp, 0xC3)
+    ks = torch.full((b, h, cap, d // g), -1.0, device=gpu)
+    vs = torch.full_like(ks, -2.0)
+    if pair:
+        _abi.int4_pack_kv_pair(k.to(gpu), v.to(gpu), kp, vp, ks, vs, pos.to(gpu), g)
+    else:
+        _abi.int4_pack_kv(k.to(gpu), kp, ks, pos.to(gpu), g)
+        _abi.int4_pack_kv(v.to(gpu), vp, vs, pos.to(gpu), g)
+    torch.cuda.synchronize()
+    for x, p_dev, s_dev, fill, sfill in ((k, kp, ks, 0x3C, -1.0), (v, vp, vs, 0xC3, -2.0)):
+        ref_p = torch.full((b, h, cap, d // 2), fill, dtype=torch.uint8)
+        ref_s = torch.full((b, h, cap, d // g), sfill)
+        oik.pack_into(ref_p, ref_s, x.contiguous(), pos, g)
         assert torch.equal(p_dev.cpu(), ref_p)
         assert torch.equal(s_dev.cpu(), ref_s)
 
