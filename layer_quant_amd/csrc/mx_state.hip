@@ -150,13 +150,28 @@ __device__ __forceinline__ void pack_block(uint32_t (&qw)[4], uint32_t (&mw)[2],
   }
 }
 
-__device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
+// lowbias32 without its last step (x ^= x >> 16): the counter mode's word formation below
+// performs that step while it makes the draws' offsets.
+__device__ __forceinline__ uint32_t lowbias32_pre(uint32_t x) {
   x ^= x >> 16;
   x *= 0x7feb352du;
   x ^= x >> 15;
   x *= 0x846ca68bu;
-  x ^= x >> 16;
   return x;
+}
+__device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
+  x = lowbias32_pre(x);
+  return x ^ (x >> 16);
+}
+
+// The two dither offsets of one hash word from x = lowbias32_pre(...): with W = x ^ (x >> 16)
+// (lowbias32's output), th = bits of 192 + (W >> 16) * 2^-16 and tl = bits of
+// 192 + (W & 0xffff) * 2^-16. th is one v_perm_b32 (x's high half under 0x4340, the bits of
+// 192.0), and tl one v_bitop3_b32 (x ^ th in the low half, th's 0x4340 in the high half): two
+// instructions where the shift, mask, xor and two ors took four.
+__device__ __forceinline__ void dither_words(uint32_t x, uint32_t& tl, uint32_t& th) {
+  th = __builtin_amdgcn_perm(sgpr_const(0x43400000u), x, 0x07060302u);
+  tl = ((x ^ th) & 0x0000ffffu) | (th & 0xffff0000u);
 }
 
 // Triton's tl.rand(seed, c) for the 64-bit offset c (triton/language/random.py, the stream of the
@@ -229,8 +244,9 @@ __device__ __forceinline__ int ceil_log2_exact(float t) {
 }
 
 // Counter-based draws of one 16-value block: element n draws counter c = rng_offset + row*N + n;
-// pair c>>1 hashes to the 32-bit word pw[k] (k = pair within the block), whose low half is the
-// even element's 16-bit draw and whose high half is the odd element's.
+// pair c>>1 hashes to the 32-bit word W = lowbias32(...) (k = pair within the block), whose low
+// half is the even element's 16-bit draw and whose high half is the odd element's; pw[k] holds
+// lowbias32_pre's value, which dither_words turns into both draws' offsets.
 __device__ __forceinline__ void block_words(uint32_t key, uint64_t c0, uint32_t (&pw)[8]) {
   const uint64_t pc0 = c0 >> 1;
   const uint32_t lo0 = (uint32_t)pc0;
@@ -246,7 +262,7 @@ __device__ __forceinline__ void block_words(uint32_t key, uint64_t c0, uint32_t 
     for (int k = 0; k < 8; ++k) kh[k] = kh0;
   }
 #pragma unroll
-  for (int k = 0; k < 8; ++k) pw[k] = lowbias32((lo0 + (uint32_t)k) ^ kh[k]);
+  for (int k = 0; k < 8; ++k) pw[k] = lowbias32_pre((lo0 + (uint32_t)k) ^ kh[k]);
 }
 
 // Shared exponent of a block from its absmax: eb = clamp(ceil(log2 t) + 127, 1, 254) with
@@ -416,8 +432,8 @@ __device__ __forceinline__ void encode16(const float (&v)[16], const float (&u16
 // byte fix turns level + 64 into the int8 level. Blocks whose exponent came from the exact rule
 // (see block_exponent), where |q| may exceed M, clamp t to [192 - M, 193 + M - 2^-16]: the same
 // levels as clamping q to [-M, M] first (floor(M + u) = M, floor(-M + u) = -M).
-// word(k) returns the hash word of pair k (its low half is the even element's draw, its high
-// half the odd element's). Each word is made just before its two fmas use it, and the next word
+// word(k) returns lowbias32_pre's value x for pair k (with W = x ^ (x >> 16), the low half of W
+// is the even element's draw and the high half the odd element's). Each word is made just before its two fmas use it, and the next word
 // waits for them: computed all at once, the eight words and the block's values were live
 // together (91 VGPRs in the reference layout's row kernel instead of 77).
 template <int FB, int LY, class WordFn>
@@ -441,9 +457,10 @@ __device__ __forceinline__ void encode16_dither(const float (&v)[16], WordFn&& w
   for (int k = 0; k < 8; ++k) {
     const bool mi = pa[k] > thr;
     const float inv = mi ? inv1 : inv0;
-    const uint32_t w = word(k);
-    t[2 * k] = __builtin_fmaf(v[2 * k], inv, __uint_as_float((w & 0xffffu) | 0x43400000u));
-    t[2 * k + 1] = __builtin_fmaf(v[2 * k + 1], inv, __uint_as_float((w >> 16) | 0x43400000u));
+    uint32_t tl, th;
+    dither_words(word(k), tl, th);
+    t[2 * k] = __builtin_fmaf(v[2 * k], inv, __uint_as_float(tl));
+    t[2 * k + 1] = __builtin_fmaf(v[2 * k + 1], inv, __uint_as_float(th));
     word.after(t[2 * k], t[2 * k + 1]);
     mb[k] = mi;
   }
@@ -487,7 +504,7 @@ struct HashWords {
     x *= 0x7feb352du;
     x ^= x >> 15;
     x *= 0x846ca68bu;
-    return x ^ (x >> 16);
+    return x;  // lowbias32_pre's value: dither_words does the last step
   }
   __device__ __forceinline__ void after(float a, float b) {
     asm volatile("" : "+v"(base) : "v"(a), "v"(b));
