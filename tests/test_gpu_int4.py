@@ -105,6 +105,29 @@ def test_pack_edge_values(gpu):
     assert ref_s[0, 0, 0, 0].item() == torch.tensor(1e-8).item()
 
 
+@pytest.mark.parametrize("g", [16, 32, 64, 128])
+def test_pack_edge_values_prompt_sized(gpu, g):
+    """The edge rows of test_pack_edge_values (a zero token, exact ties, 1e-30 and 3e37 values)
+    inside a prompt of 64 tokens, so that the group-per-lane kernel (g 16 / 32 / 64) and the row
+    kernel (g 128) quantise them: bit-exact against the oracle."""
+    d, t = 128, 64
+    gen = torch.Generator().manual_seed(g)
+    x = torch.randn(2, 2, t, d, generator=gen)
+    x[0, 0, 0] = 0
+    x[0, 0, 1, :8] = torch.tensor([7.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5])
+    x[0, 1, 2] = torch.randn(d, generator=gen) * 1e-30
+    x[1, 0, 3] = torch.randn(d, generator=gen) * 3e37
+    x[1, 1, 5, ::g] = 7.0 * 2.0 ** -130  # a subnormal group maximum
+    pos = torch.arange(t)
+    packed = torch.zeros(2, 2, t, d // 2, dtype=torch.uint8, device=gpu)
+    scale = torch.zeros(2, 2, t, d // g, device=gpu)
+    _abi.int4_pack_kv(x.to(gpu), packed, scale, pos.to(gpu), g)
+    ref_p = torch.zeros(2, 2, t, d // 2, dtype=torch.uint8)
+    ref_s = torch.zeros(2, 2, t, d // g)
+    oik.pack_into(ref_p, ref_s, x, pos, g)
+    assert torch.equal(packed.cpu(), ref_p) and torch.equal(scale.cpu(), ref_s)
+
+
 @pytest.mark.parametrize("g,d", [(8, 128), (16, 128), (32, 128), (64, 128), (128, 128),
                                  (256, 256), (32, 64)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
