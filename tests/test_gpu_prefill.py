@@ -68,6 +68,28 @@ def test_prefill_parity_mfma_and_generic(gpu, b, hkv, nrep, L, g):
     assert_close_rel(_run(gpu, cache, q.float(), nrep, g), ref, what="generic")
 
 
+@pytest.mark.parametrize("span", [10, 13])
+@pytest.mark.parametrize("b,hkv,nrep,L,g", [(1, 2, 4, 200, 32), (2, 2, 4, 100, 64)])
+def test_prefill_wide_value_scale_span(gpu, b, hkv, nrep, L, g, span):
+    """Each key's values scaled by 2^-u, u uniform in [0, span): a group's V scales span up to
+    2^span across a workgroup's keys, so P' = p * vscale / vmax reaches down to 2^-span times p,
+    which the MFMA kernel's fp16 hi + lo split must still carry to the 2e-3 bar (the stated limit
+    of the split is a span of 2^14)."""
+    d = 128
+    gen = torch.Generator().manual_seed(1000 + span + L)
+    cache = oik.allocate_cache(b, hkv, L + 7, d, g)
+    k = _activations((b, hkv, L, d), 1100 + L)
+    v = _activations((b, hkv, L, d), 1101 + L).float()
+    v = (v * torch.exp2(-torch.rand(b, hkv, L, 1, generator=gen) * span)).to(torch.bfloat16)
+    oik.pack_kv_into_cache(cache, k, v, torch.arange(L), g)
+    vs = cache["v_scale"][:, :, :L]
+    assert (vs.amax() / vs.amin()).item() > 2.0 ** (span - 2)
+    q = _activations((b, hkv * nrep, L, d), 1150 + L)
+    ref = _oracle(cache, q, nrep, g)
+    assert_close_rel(_run(gpu, cache, q, nrep, g), ref, what="mfma")
+    assert_close_rel(_run(gpu, cache, q.float(), nrep, g), ref, what="generic")
+
+
 @pytest.mark.parametrize("b,hkv,nrep,L,g,d", [(1, 2, 4, 90, 16, 128), (2, 1, 2, 40, 32, 64),
                                               (1, 1, 3, 33, 64, 256)])
 def test_prefill_generic_shapes(gpu, b, hkv, nrep, L, g, d):
