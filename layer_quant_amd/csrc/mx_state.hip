@@ -926,8 +926,16 @@ __device__ __forceinline__ void update_rows(const MxUpdateParams& p, const HeadB
 // One work item per workgroup: grid (ceil(P / (R * SLOTS)), H, B). Every state load of the lane
 // (R state blocks, x, z) is issued before the first use of any of them; B, C and the head scalars
 // come through LDS (one barrier).
+// The byte-mantissa compact layout (CM8) asks for 6 waves per SIMD: its 4-row form then fits 77-79
+// VGPRs without spills instead of taking 84 (5 waves); MX8 at batch 64, three alternated rounds on
+// one box: 35.71-35.91 against 36.60-37.33 us. Its supplied-uniform form (2 rows, 256 threads)
+// would spill under the cap and keeps the default, as do the other layouts (the nibble layout's
+// MX4 form spills at 6 waves).
+constexpr int rows_waves(int LY, int RMODE) {
+  return LY == LAYOUT_CM8 && RMODE != LQ_ROUND_SR_UNIFORM ? 6 : LQ_MX_ROWS_WAVES;
+}
 template <int FB, int RMODE, int BPR_LOG2, int R, int THREADS, int LY>
-__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(LQ_MX_ROWS_WAVES)))
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(rows_waves(LY, RMODE))))
 void mx_update_rows_kernel(MxUpdateParams p) {
   constexpr int BPR = 1 << BPR_LOG2;
   constexpr uint32_t N = 16 * BPR;
